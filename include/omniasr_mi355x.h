@@ -1,0 +1,189 @@
+/*
+ * omniasr_mi355x.h -- C ABI of the MI355X (gfx950) kernels of omniasr-trt's speculative greedy
+ * decoder step.
+ *
+ * The reference's boundary is the Python module ``omniasr_trt.kernels``: functions taking torch
+ * tensors and launching Triton kernels on torch's current stream. This library replaces those
+ * kernels; each entry point below names the reference function (file:line, relative to the
+ * reference repository) whose work it does. The Python shim ``omniasr-trt_amd/kernels.py`` keeps
+ * the reference's function signatures and calls these entry points with raw device pointers.
+ *
+ * Conventions shared by every entry point:
+ *   - pointers are device pointers; sizes, strides and positions are int64 (token buffers int32,
+ *     flags uint8 holding 0/1 -- torch.bool's layout), strides count elements, not bytes;
+ *   - ``stream`` is a hipStream_t (NULL: the default stream); nothing synchronises the host and
+ *     nothing allocates, so every call can be captured into a HIP graph;
+ *   - the return value is OMNI_OK, a negative OMNI_ERR_* for an argument the kernels do not cover
+ *     (checked before anything is launched), or a positive hipError_t from the launch;
+ *   - indices read from device memory (positions, cache rows, lengths) are clamped or skipped where
+ *     they would leave a buffer, so a wrong index never makes a kernel touch memory outside the
+ *     arguments' extents (the reference's behaviour there is undefined).
+ */
+#ifndef OMNIASR_MI355X_H
+#define OMNIASR_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OMNI_OK 0
+#define OMNI_ERR_INVALID (-1)   /* null pointer, negative size, misaligned or too small stride */
+#define OMNI_ERR_DTYPE (-2)     /* element type the kernels are not built for */
+#define OMNI_ERR_SHAPE (-3)     /* head_dim / tokens / window beyond what the kernels cover */
+#define OMNI_ERR_WORKSPACE (-4) /* workspace smaller than omni_verify_attention_workspace() */
+
+#define OMNI_F32 0
+#define OMNI_BF16 1
+
+/* verify-attention flags */
+#define OMNI_ATTN_SEPARATE_COMBINE 1 /* merge key splits in a second launch, not in the last split */
+
+/* Human-readable text of a status code (static storage). */
+const char *omni_status_string(int status);
+
+/* ABI version of this header (bumped on any signature change). */
+int omni_abi_version(void);
+
+/*
+ * RoPE + KV-cache append.  Replaces ``kernels.rope_kv`` / ``_rope_kv``
+ * (src/omniasr_trt/kernels.py:294-306, 31-54) with the rotation of ``apply_rope``
+ * (src/omniasr_trt/modeling.py:301-306).
+ *
+ * Token n (0 <= n < n_tokens) of ``qkv`` [n_tokens, 3*heads*head_dim] (q | k | v, row stride
+ * ``qkv_row_stride``) is rotated at position pos[n]: interleaved pairs (re, im) of q and k become
+ * (re*c - im*s, re*s + im*c) in fp32 with c, s = cs[pos[n], j] (``cs`` [cs_rows, head_dim/2, 2]
+ * fp32), each product rounded on its own (no fused multiply-add), then rounded to the element
+ * type (bf16: nearest even).  The rotated q goes to ``q_out`` [n_tokens, heads, head_dim]; the
+ * rotated k and the unrotated v go to cache row slots[n] (NULL: n), position cache_pos[n] (NULL:
+ * pos[n]) of ``k_cache`` / ``v_cache`` (strides row / head / position, unit stride in head_dim).
+ * head_dim: a multiple of 8.  dtype: OMNI_BF16 or OMNI_F32.
+ */
+int omni_rope_kv_append(const void *qkv, int64_t qkv_row_stride, const float *cs, int64_t cs_rows,
+                        const int64_t *pos, const int64_t *slots, const int64_t *cache_pos,
+                        void *q_out, void *k_cache, void *v_cache, int64_t stride_row,
+                        int64_t stride_head, int64_t stride_pos, int64_t cache_rows,
+                        int64_t cache_len, int64_t n_tokens, int32_t heads, int32_t head_dim,
+                        int32_t dtype, void *stream);
+
+/*
+ * Key-split size (keys per split, a multiple of 32) that omni_verify_attention uses when called
+ * with chunk = 0, for this launch shape.
+ */
+int32_t omni_verify_attention_chunk(int32_t rows, int32_t tokens, int32_t heads, int32_t head_dim,
+                                    int32_t keys);
+
+/* Bytes of workspace omni_verify_attention needs for this shape and split size (0: default). */
+size_t omni_verify_attention_workspace(int32_t rows, int32_t tokens, int32_t heads,
+                                       int32_t head_dim, int32_t keys, int32_t chunk);
+
+/*
+ * Multi-query split-K flash-decode verification attention.  Replaces ``kernels.draft_attention``
+ * (``_beam_ctx`` with CAUSAL=True + ``_beam_combine``, src/omniasr_trt/kernels.py:338-358, 56-113,
+ * 146-161) and, at tokens = 1, ``kernels.decode_attention`` (``_attn_split`` + ``_attn_combine``,
+ * src/omniasr_trt/kernels.py:406-423, 163-211).
+ *
+ * ``q`` [rows*tokens, heads, head_dim] contiguous: row b's ``tokens`` queries are rows
+ * b*tokens .. b*tokens+tokens-1.  Query i of row b attends to keys [0, lengths[b] + i) of cache
+ * row b (``k_cache`` / ``v_cache`` with strides row / head / position, unit stride in head_dim,
+ * ``cache_len`` positions): out = softmax(q.k * scale) . v, accumulated in fp32; an empty key range
+ * gives zeros.  All keys must lie within the first ``keys`` positions (the graph bucket); the launch
+ * grid depends on ``keys`` only.  One pass over a row's keys serves all of its queries.
+ * ``chunk``: keys per split (a multiple of 32; 0: omni_verify_attention_chunk()).
+ * ``workspace``: at least omni_verify_attention_workspace() bytes, 256-byte aligned, any content.
+ * ``counters``: rows*heads int32, zero before the first call; every call leaves them zero (calls
+ * that share them must not overlap in time).
+ * bf16: head_dim a multiple of 128 runs on MFMA, any other multiple of 8 on the vector ALUs;
+ * f32: vector ALUs (fp32 products).  tokens: 1..16.
+ */
+int omni_verify_attention(const void *q, const void *k_cache, const void *v_cache,
+                          int64_t stride_row, int64_t stride_head, int64_t stride_pos,
+                          int64_t cache_len, const int64_t *lengths, int32_t rows, int32_t tokens,
+                          int32_t heads, int32_t head_dim, int32_t keys, int32_t chunk, float scale,
+                          void *out, void *workspace, size_t workspace_bytes, int32_t *counters,
+                          int32_t flags, int32_t dtype, void *stream);
+
+/*
+ * Draft proposal of every row.  Replaces ``kernels.propose`` / ``_propose``
+ * (src/omniasr_trt/kernels.py:361-377, 214-268) as called by ``SpecDecoder.propose``
+ * (src/omniasr_trt/spec.py:76-80).
+ *
+ * Row b: the newest ``ngram`` tokens out[b, last[b] - t] (valid while >= first[b]) are matched
+ * against ``anchor_width`` draft anchors (offset i - behind from next[b] - 1, live while the offset
+ * is <= ahead and the anchor < draft_len[b]) and ``self_width`` earlier own positions
+ * (last[b] - 1 - i, live while >= first[b]); a draft anchor needs reach[r][1] matching tokens
+ * within distance reach[r][0] (r = 0..3, else ngram); the best anchor ranks score*256 - distance
+ * (first on ties), the best own position is the latest with the most matches.  Writes prop[b, 0..k)
+ * (int64), use_draft[b] and start[b] (draft position of the first proposal).
+ * ``out`` [rows, out_stride] int32 (out_cap positions), ``draft`` [rows, draft_stride] int32
+ * (draft_cap entries).  k <= 64, ngram <= 64, anchor_width and self_width <= 4096.
+ */
+int omni_propose(const int32_t *out, int64_t out_stride, int64_t out_cap, const int32_t *draft,
+                 int64_t draft_stride, int64_t draft_cap, const int64_t *draft_len,
+                 const int64_t *last, const int64_t *first, const int64_t *next, int64_t *prop,
+                 uint8_t *use_draft, int64_t *start, int32_t rows, int32_t k, int32_t ngram,
+                 int32_t behind, int32_t ahead, int32_t anchor_width, int32_t self_width,
+                 int32_t self_min, const int32_t reach[8], void *stream);
+
+/*
+ * omni_propose plus the assembly of a drafted step's inputs, in the same launch.  Replaces
+ * ``SpecDecoder.propose`` and the torch operations of ``SpecDecoder.step`` that build the fed
+ * tokens, positions, cache rows and key counts (src/omniasr_trt/spec.py:85-95):
+ *   running = !done[b]; p = last[b] + running;
+ *   tokens[b] = (tok[b], prop[b, 0..k));             [rows, k+1] int64
+ *   pos[b*(k+1) + j] = min(running ? p + j : last[b], capacity - 1);
+ *   slots[b*(k+1) + j] = b;  lengths[b] = running ? p + 1 : 0.
+ * ``prop`` may be NULL (the proposals then only land in ``tokens``).
+ */
+int omni_spec_prepare(const int32_t *out, int64_t out_stride, int64_t out_cap,
+                      const int32_t *draft, int64_t draft_stride, int64_t draft_cap,
+                      const int64_t *draft_len, const int64_t *last, const int64_t *first,
+                      const int64_t *next, int64_t *prop, uint8_t *use_draft, int64_t *start,
+                      int32_t rows, int32_t k, int32_t ngram, int32_t behind, int32_t ahead,
+                      int32_t anchor_width, int32_t self_width, int32_t self_min,
+                      const int32_t reach[8], const int64_t *tok, const uint8_t *done,
+                      int64_t capacity, int64_t *tokens, int64_t *pos, int64_t *slots,
+                      int64_t *lengths, void *stream);
+
+/*
+ * Greedy acceptance and rollback of a drafted step, from the argmaxes.  Replaces
+ * ``kernels.accept`` / ``_accept`` (src/omniasr_trt/kernels.py:380-390, 271-291).
+ *
+ * Row b with done[b] == 0: p = last[b] + 1, g_j = nxt[b, j]; kept = the number of leading j with
+ * tokens[b, j+1] == g_j (at most T-1); stop_j = (g_j == eos or p + j >= limit) and j <= kept;
+ * n = the first j with stop_j, else kept.  Writes out[b, min(p + j, out_cap - 1)] = g_j for
+ * j <= n, tok[b] = g_n, last[b] = p + n, done[b] = any stop_j and, when draft_next is not NULL,
+ * draft_next[b] = (use_draft[b] ? start[b] : draft_next[b]) + n + 1.  Finished rows are untouched.
+ * The cache is rolled back by the length alone: nothing is erased.  T: 1..64.
+ */
+int omni_accept(const int64_t *tokens, const int64_t *nxt, int32_t *out, int64_t out_stride,
+                int64_t out_cap, int64_t *tok, int64_t *last, uint8_t *done, int64_t *draft_next,
+                const int64_t *start, const uint8_t *use_draft, int32_t rows, int32_t tokens_per_row,
+                int64_t limit, int64_t eos, void *stream);
+
+/*
+ * Verify logits -> greedy argmax -> acceptance, in one launch.  Replaces
+ * ``F.log_softmax(logits, -1).argmax(-1)`` of the drafted step (src/omniasr_trt/spec.py:106-107)
+ * and of the one-token step (src/omniasr_trt/decode.py:218-224), followed by omni_accept.
+ *
+ * ``logits`` [rows*T, vocab] (row stride ``logits_stride``, element type ``logits_dtype``): the
+ * argmax of row r is the first index i where the log-softmax, computed as PyTorch's does
+ * ((x_i - max) - log(sum_j exp(x_j - max)) in fp32, then rounded to the logits' type), reaches its
+ * maximum.  It is written to nxt[r] (int64) when ``nxt`` is not NULL, then every row is accepted as
+ * by omni_accept.  ``start``, ``use_draft`` and ``draft_next`` may be NULL together (the one-token
+ * step).  T: 1..64.
+ */
+int omni_greedy_accept(const void *logits, int64_t logits_stride, int32_t vocab,
+                       int32_t logits_dtype, const int64_t *tokens, int64_t *nxt, int32_t *out,
+                       int64_t out_stride, int64_t out_cap, int64_t *tok, int64_t *last,
+                       uint8_t *done, int64_t *draft_next, const int64_t *start,
+                       const uint8_t *use_draft, int32_t rows, int32_t tokens_per_row,
+                       int64_t limit, int64_t eos, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OMNIASR_MI355X_H */

@@ -1,0 +1,307 @@
+"""The decode-step kernels of the omniASR LLM decoder on MI355X (gfx950), behind omniasr-trt's API.
+
+Same functions, arguments and results as ``omniasr_trt.kernels`` (src/omniasr_trt/kernels.py), so the
+decoders above it are unchanged; each one calls a hand-written HIP kernel of ``libomniasr_mi355x.so``
+through its C ABI (``include/omniasr_mi355x.h``) on torch's current stream:
+
+* :func:`rope_kv` -- RoPE of q and k at each token's position, k and v written into the KV cache
+  (``omni_rope_kv_append``);
+* :func:`draft_attention` -- the verify attention of a drafted step: a row's T queries over its own
+  keys, causal among the new ones, one read of the keys for all of them; :func:`decode_attention` is
+  its one-query case (``omni_verify_attention``);
+* :func:`propose` -- the draft proposal of every row (``omni_propose``);
+* :func:`accept` -- greedy acceptance and rollback (``omni_accept``).
+
+Beyond the reference's functions, for the fused step: :func:`spec_prepare` (proposal plus the step's
+tokens / positions / cache rows / key counts in one launch) and :func:`greedy_accept` (the argmax of
+the verify logits and the acceptance in one launch).
+
+Nothing here synchronises or allocates beyond the outputs and the attention workspace (from torch's
+allocator, so from a graph's pool under capture), so every function can be captured in a HIP graph.
+There is no other code path: on a GPU without the library these functions raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+# Launch settings of draft_attention / decode_attention: ``chunk`` keys per split (0: the library's
+# choice for the launch shape), ``separate``: merge the splits in a second launch (else the last
+# split of each row and head merges them).
+DRAFT_ATTN = {"chunk": 0, "separate": False}
+ATTN = {"chunk": 0, "separate": False}
+
+_counters: dict[int, torch.Tensor] = {}
+# Ticket buffers replaced by larger ones: captured graphs may still hold their addresses, so they
+# live as long as the process.
+_retired: list[torch.Tensor] = []
+
+
+def available(device: torch.device) -> bool:
+    """True on a GPU device (the library is loaded; a missing library raises), False elsewhere."""
+    device = torch.device(device)
+    if device.type != "cuda":
+        return False
+    _lib.load()
+    return True
+
+
+def _dtype(t: torch.Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return _lib.BF16
+    if t.dtype == torch.float32:
+        return _lib.F32
+    raise TypeError(f"the HIP kernels take bfloat16 or float32, not {t.dtype}")
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def _need(cond: bool, what: str) -> None:
+    if not cond:
+        raise ValueError(what)
+
+
+def _index(t: torch.Tensor, name: str) -> None:
+    _need(t.dtype == torch.long and t.is_contiguous() and t.is_cuda, f"{name}: contiguous int64 on the GPU")
+
+
+def next_power_of_2(n: int) -> int:
+    return 1 if n <= 1 else 1 << (int(n) - 1).bit_length()
+
+
+def rope_kv(qkv: torch.Tensor, cs: torch.Tensor, pos: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+            heads: int, slots: torch.Tensor | None = None, cache_pos: torch.Tensor | None = None) -> torch.Tensor:
+    """``qkv`` [N, 3*H*D] (q|k|v of N tokens), ``cs`` [P, D/2, 2] fp32, ``pos`` [N]; ``k_cache``/``v_cache``
+    [rows, H, S, D] with unit stride in D.  Rotates at ``pos[n]`` and writes token n's k, v at cache row
+    ``slots[n]`` (default n), position ``cache_pos[n]`` (default ``pos[n]``); returns the rotated q [N, H, D].
+    (src/omniasr_trt/kernels.py:294-306)"""
+    lib = _lib.load()
+    n = qkv.size(0)
+    dim = qkv.size(1) // (3 * heads)
+    _need(qkv.dim() == 2 and qkv.stride(1) == 1, "qkv: [N, 3*H*D] with unit stride in the last dimension")
+    _need(k_cache.dtype == qkv.dtype == v_cache.dtype, "qkv and the caches: one dtype")
+    _need(k_cache.stride() == v_cache.stride() and k_cache.shape == v_cache.shape, "k_cache / v_cache: same layout")
+    _need(k_cache.dim() == 4 and k_cache.stride(3) == 1 and k_cache.size(3) == dim, "caches: [rows, H, S, D]")
+    _need(cs.dtype == torch.float32 and cs.is_contiguous() and cs.size(-2) * 2 == dim, "cs: [P, D/2, 2] fp32")
+    _index(pos, "pos")
+    for name, t in (("slots", slots), ("cache_pos", cache_pos)):
+        if t is not None:
+            _index(t, name)
+    q = torch.empty(n, heads, dim, device=qkv.device, dtype=qkv.dtype)
+    status = lib.omni_rope_kv_append(
+        qkv.data_ptr(), qkv.stride(0), cs.data_ptr(), cs.size(0), pos.data_ptr(), _ptr(slots), _ptr(cache_pos),
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
+        k_cache.stride(2), k_cache.size(0), k_cache.size(2), n, heads, dim, _dtype(qkv), _stream(qkv))
+    _lib.check(status, "rope_kv")
+    return q
+
+
+def _attn_counters(device: torch.device, n: int) -> torch.Tensor:
+    """Per-(row, head) tickets of the split merge: zero, and left zero by every call."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    have = _counters.get(idx)
+    if have is None or have.numel() < n:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("verify attention: its tickets must be allocated before graph capture "
+                               "(run the step once outside the capture)")
+        size = max(n, 1 << 16, 0 if have is None else 2 * have.numel())
+        if have is not None:
+            _retired.append(have)
+        _counters[idx] = have = torch.zeros(size, device=device, dtype=torch.int32)
+    return have
+
+
+def _verify(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor, tokens: int,
+            keys: int, scale: float, chunk: int, separate: bool) -> torch.Tensor:
+    lib = _lib.load()
+    rows_total, heads, dim = q.shape
+    _need(rows_total % tokens == 0, "q: [B*T, H, D]")
+    groups = rows_total // tokens
+    _need(q.is_contiguous(), "q: contiguous [B*T, H, D]")
+    _need(k_cache.dtype == q.dtype == v_cache.dtype, "q and the caches: one dtype")
+    _need(k_cache.stride() == v_cache.stride() and k_cache.shape == v_cache.shape, "k_cache / v_cache: same layout")
+    _need(k_cache.dim() == 4 and k_cache.stride(3) == 1 and k_cache.size(3) == dim, "caches: [>=B, H, S, D]")
+    _need(k_cache.size(0) >= groups and k_cache.size(1) == heads, "caches: at least B rows of H heads")
+    _index(lengths, "lengths")
+    _need(lengths.numel() >= groups, "lengths: [B]")
+    chunk = int(chunk or 0)
+    ws = lib.omni_verify_attention_workspace(groups, tokens, heads, dim, keys, chunk)
+    workspace = torch.empty(max(ws, 256), device=q.device, dtype=torch.uint8)
+    counters = _attn_counters(q.device, groups * heads)
+    out = torch.empty_like(q)
+    flags = _lib.ATTN_SEPARATE_COMBINE if separate else 0
+    status = lib.omni_verify_attention(
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
+        k_cache.stride(2), k_cache.size(2), lengths.data_ptr(), groups, tokens, heads, dim, keys, chunk,
+        float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel(), counters.data_ptr(), flags,
+        _dtype(q), _stream(q))
+    _lib.check(status, "verify attention")
+    return out
+
+
+def draft_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor,
+                    tokens: int, keys: int, scale: float, **launch) -> torch.Tensor:
+    """Draft verification: ``q`` [B*T, H, D], row b's T queries at rows b*T .. b*T+T-1; query i of row b attends to
+    keys [0, lengths[b] + i) of cache row b (``k_cache``/``v_cache`` [>=B, H, S, D], all within the first ``keys``).
+    One K/V read serves all T queries of a row.  Returns [B*T, H, D] in q's dtype.  ``launch``: overrides of
+    ``DRAFT_ATTN`` (the reference's Triton settings -- block, warps, stages, programs -- have no meaning here and
+    are ignored).  (src/omniasr_trt/kernels.py:338-358)"""
+    cfg = {**DRAFT_ATTN, **{k: v for k, v in launch.items() if k in DRAFT_ATTN}}
+    return _verify(q, k_cache, v_cache, lengths, tokens, keys, scale, cfg["chunk"], cfg["separate"])
+
+
+def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor,
+                     keys: int, scale: float, block: int | None = None, warps: int | None = None,
+                     stages: int | None = None, programs: int | None = None, chunk: int | None = None) -> torch.Tensor:
+    """``q`` [B, H, D]; ``k_cache``/``v_cache`` [>=B, H, S, D]; row r attends to keys [0, lengths[r]) (all within the
+    first ``keys``, which fixes the launch grid).  Returns [B, H, D] in q's dtype.  ``block`` / ``warps`` /
+    ``stages`` / ``programs`` are the reference's Triton settings, accepted and ignored.
+    (src/omniasr_trt/kernels.py:406-423)"""
+    del block, warps, stages, programs
+    return _verify(q, k_cache, v_cache, lengths, 1, keys, scale, ATTN["chunk"] if chunk is None else chunk,
+                   ATTN["separate"])
+
+
+def splits_for(rows: int, heads: int, keys: int, block: int = 64, programs: int = 264) -> tuple[int, int]:
+    """Key splits (a power of two, about ``programs`` programs in all) and the keys each split covers -- the
+    reference's rule for its Triton launches (src/omniasr_trt/kernels.py:393-400), kept for callers that use it;
+    the HIP launches choose their split with :func:`verify_chunk`."""
+    want = max(1, programs // (rows * heads))
+    splits = 1
+    while splits * 2 <= want and splits * 2 * block <= keys:
+        splits *= 2
+    chunk = -(-keys // splits)
+    return splits, -(-chunk // block) * block
+
+
+def verify_chunk(rows: int, tokens: int, heads: int, head_dim: int, keys: int) -> int:
+    """Keys per split of the verify attention at this launch shape (``omni_verify_attention_chunk``)."""
+    return int(_lib.load().omni_verify_attention_chunk(rows, tokens, heads, head_dim, keys))
+
+
+def _reach(reach) -> ctypes.Array:
+    flat = [int(x) for pair in reach for x in pair]
+    _need(len(flat) == 8, "reach: four (distance, tokens) pairs")
+    return (ctypes.c_int32 * 8)(*flat)
+
+
+def _propose_args(out, draft, draft_len, last, first, nxt, start, tokens, ngram, behind, ahead, reach, self_window,
+                  self_min):
+    _need(out.dtype == torch.int32 and out.stride(1) == 1, "out: [>=B, S] int32")
+    _need(draft.dtype == torch.int32 and draft.stride(1) == 1, "draft: [>=B, C] int32")
+    for name, t in (("draft_len", draft_len), ("last", last), ("first", first), ("next", nxt), ("start", start)):
+        _index(t, name)
+    width = next_power_of_2(behind + ahead + 1)  # the reference's anchor lanes (kernels.py:375)
+    self_width = next_power_of_2(self_window)
+    return [out.data_ptr(), out.stride(0), out.size(1), draft.data_ptr(), draft.stride(0), draft.size(1),
+            draft_len.data_ptr(), last.data_ptr(), first.data_ptr(), nxt.data_ptr()], \
+        [tokens, ngram, behind, ahead, width, self_width, self_min, _reach(reach)]
+
+
+def propose(out: torch.Tensor, draft: torch.Tensor, draft_len: torch.Tensor, last: torch.Tensor,
+            first: torch.Tensor, nxt: torch.Tensor, start: torch.Tensor, tokens: int, ngram: int, behind: int,
+            ahead: int, reach: tuple, self_window: int, self_min: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Drafted decoding's proposals of rows 0..B-1 (B = ``last.numel()``): ``tokens`` ids each [B, k] (int64) and
+    whether they come from the draft [B] (else from the row's own tokens); ``start`` [B] gets the draft position of
+    the first one.  ``out`` [>=B, S] int32 generated tokens by position, ``draft`` [>=B, C] int32; ``draft_len``,
+    ``last``, ``first``, ``nxt`` [B] int64.  (src/omniasr_trt/kernels.py:361-377)"""
+    lib = _lib.load()
+    b = last.numel()
+    head, tail = _propose_args(out, draft, draft_len, last, first, nxt, start, tokens, ngram, behind, ahead, reach,
+                               self_window, self_min)
+    prop = torch.empty(b, tokens, device=out.device, dtype=torch.long)
+    use_draft = torch.empty(b, device=out.device, dtype=torch.bool)
+    status = lib.omni_propose(*head, prop.data_ptr(), use_draft.data_ptr(), start.data_ptr(), b, *tail,
+                              _stream(out))
+    _lib.check(status, "propose")
+    return prop, use_draft
+
+
+def spec_prepare(out: torch.Tensor, draft: torch.Tensor, draft_len: torch.Tensor, last: torch.Tensor,
+                 first: torch.Tensor, nxt: torch.Tensor, start: torch.Tensor, tok: torch.Tensor, done: torch.Tensor,
+                 capacity: int, tokens: int, ngram: int, behind: int, ahead: int, reach: tuple, self_window: int,
+                 self_min: int):
+    """:func:`propose` and the drafted step's inputs in one launch (src/omniasr_trt/spec.py:85-95).  Returns the
+    fed tokens [B, k+1] (the newest token, then the proposal), positions and cache rows [B*(k+1)], key counts [B]
+    (0 for finished rows) and ``use_draft`` [B]; ``start`` is written as by :func:`propose`."""
+    lib = _lib.load()
+    b = last.numel()
+    head, tail = _propose_args(out, draft, draft_len, last, first, nxt, start, tokens, ngram, behind, ahead, reach,
+                               self_window, self_min)
+    _index(tok, "tok")
+    _need(done.dtype == torch.bool and done.is_contiguous(), "done: bool [B]")
+    width = tokens + 1
+    dev = out.device
+    fed = torch.empty(b, width, device=dev, dtype=torch.long)
+    pos = torch.empty(b * width, device=dev, dtype=torch.long)
+    slots = torch.empty(b * width, device=dev, dtype=torch.long)
+    lengths = torch.empty(b, device=dev, dtype=torch.long)
+    use_draft = torch.empty(b, device=dev, dtype=torch.bool)
+    status = lib.omni_spec_prepare(*head, None, use_draft.data_ptr(), start.data_ptr(), b, *tail, tok.data_ptr(),
+                                   done.data_ptr(), int(capacity), fed.data_ptr(), pos.data_ptr(), slots.data_ptr(),
+                                   lengths.data_ptr(), _stream(out))
+    _lib.check(status, "spec_prepare")
+    return fed, pos, slots, lengths, use_draft
+
+
+def _state_args(out, tok, last, done, draft_next, start, use_draft):
+    _need(out.dtype == torch.int32 and out.stride(1) == 1, "out: [>=B, S] int32")
+    for name, t in (("tok", tok), ("last", last)):
+        _index(t, name)
+    _need(done.dtype == torch.bool and done.is_contiguous(), "done: bool [B]")
+    if draft_next is not None:
+        _index(draft_next, "draft_next")
+        _index(start, "start")
+        _need(use_draft.dtype == torch.bool and use_draft.is_contiguous(), "use_draft: bool [B]")
+    return [out.data_ptr(), out.stride(0), out.size(1), tok.data_ptr(), last.data_ptr(), done.data_ptr(),
+            _ptr(draft_next), _ptr(start), _ptr(use_draft)]
+
+
+def accept(tokens: torch.Tensor, nxt: torch.Tensor, out: torch.Tensor, tok: torch.Tensor, last: torch.Tensor,
+           done: torch.Tensor, draft_next: torch.Tensor, start: torch.Tensor, use_draft: torch.Tensor, limit: int,
+           eos: int) -> None:
+    """In place on rows 0..B-1 after a drafted step: ``tokens`` fed [B, T] (the newest token, then the proposal) and
+    ``nxt`` the argmax after each [B, T] (int64); ``out`` [>=B, S] int32, ``tok``/``last``/``draft_next``/``start``
+    [B] int64, ``done``/``use_draft`` [B] bool.  A running row keeps argmax 0..n (n: its leading proposed tokens
+    equal to the argmax before them, or the first EOS / position >= ``limit`` among those) at positions
+    ``last + 1 + j``.  (src/omniasr_trt/kernels.py:380-390)"""
+    lib = _lib.load()
+    b, width = tokens.shape
+    _index(tokens, "tokens")
+    _index(nxt, "nxt")
+    state = _state_args(out, tok, last, done, draft_next, start, use_draft)
+    status = lib.omni_accept(tokens.data_ptr(), nxt.data_ptr(), *state, b, width, int(limit), int(eos),
+                             _stream(tokens))
+    _lib.check(status, "accept")
+
+
+def greedy_accept(logits: torch.Tensor, tokens: torch.Tensor, out: torch.Tensor, tok: torch.Tensor,
+                  last: torch.Tensor, done: torch.Tensor, draft_next: torch.Tensor | None,
+                  start: torch.Tensor | None, use_draft: torch.Tensor | None, limit: int, eos: int,
+                  nxt: torch.Tensor | None = None) -> torch.Tensor:
+    """``F.log_softmax(logits, -1).argmax(-1)`` of the verify logits [B*T, V] followed by :func:`accept`, in one
+    launch (src/omniasr_trt/spec.py:106-108).  Returns the argmaxes [B, T] (written into ``nxt`` when given).
+    ``draft_next`` / ``start`` / ``use_draft`` None: the one-token step's update (src/omniasr_trt/decode.py:218-224)."""
+    lib = _lib.load()
+    b, width = tokens.shape
+    _index(tokens, "tokens")
+    _need(logits.dim() == 2 and logits.size(0) == b * width and logits.stride(1) == 1, "logits: [B*T, V]")
+    if nxt is None:
+        nxt = torch.empty(b, width, device=logits.device, dtype=torch.long)
+    _index(nxt, "nxt")
+    state = _state_args(out, tok, last, done, draft_next, start, use_draft)
+    status = lib.omni_greedy_accept(logits.data_ptr(), logits.stride(0), logits.size(1), _dtype(logits),
+                                    tokens.data_ptr(), nxt.data_ptr(), *state, b, width, int(limit), int(eos),
+                                    _stream(logits))
+    _lib.check(status, "greedy_accept")
+    return nxt

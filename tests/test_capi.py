@@ -1,0 +1,97 @@
+"""The C ABI (CPU): the library loads and exports every entry point include/omniasr_mi355x.h declares, and the
+argument checks that run before any launch answer with the documented status codes.  No kernel is launched."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from omniasr_trt_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "omniasr_mi355x.h"
+
+
+def declared() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(omni_\w+)\s*\(", text))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _lib.load()
+    names = declared()
+    assert {"omni_rope_kv_append", "omni_verify_attention", "omni_propose", "omni_accept",
+            "omni_greedy_accept", "omni_spec_prepare"} <= names
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(_lib.symbols()) == names  # the shim binds exactly what the header declares
+
+
+def test_abi_version_and_status_text():
+    lib = _lib.load()
+    assert lib.omni_abi_version() == _lib.ABI_VERSION
+    assert _lib.status_string(0) == "ok"
+    for code in (-1, -2, -3, -4):
+        assert _lib.status_string(code) not in ("ok", "unknown status")
+
+
+def test_workspace_and_split_queries():
+    lib = _lib.load()
+    for rows, t, h, d, keys in ((8, 5, 32, 128, 2560), (8, 1, 8, 512, 2048), (1, 9, 32, 128, 1280), (4, 3, 2, 16, 256)):
+        chunk = lib.omni_verify_attention_chunk(rows, t, h, d, keys)
+        assert chunk % 64 == 0 and 64 <= chunk <= max(64, -(-keys // 32) * 32)
+        splits = -(-keys // chunk)
+        units = rows * h * splits * t
+        want = -(-units * d * 4 // 256) * 256 + -(-units * 2 * 4 // 256) * 256
+        assert lib.omni_verify_attention_workspace(rows, t, h, d, keys, 0) == want
+    # config 3: 8 rows x 32 heads, keys 2560 -> about 2048 waves over the chip
+    assert lib.omni_verify_attention_chunk(8, 5, 32, 128, 2560) == 320
+
+
+FAKE = ctypes.c_void_p(0x10000)  # never dereferenced: every call below fails its checks before any launch
+
+
+def test_argument_errors_before_launch():
+    lib = _lib.load()
+    # verify attention: 17 queries per row, an fp16 dtype, a too-small workspace
+    args = [FAKE, FAKE, FAKE, 1 << 20, 1 << 16, 128, 4096, FAKE, 8, 17, 32, 128, 2560, 0, 0.1, FAKE, FAKE, 1 << 30,
+            FAKE, 0, _lib.BF16, None]
+    assert lib.omni_verify_attention(*args) == -3
+    args[9] = 5
+    args[-2] = 7
+    assert lib.omni_verify_attention(*args) == -2
+    args[-2] = _lib.BF16
+    args[17] = 16
+    assert lib.omni_verify_attention(*args) == -4
+    args[17] = 1 << 30
+    args[13] = 100  # a split that is not a multiple of 64 keys
+    assert lib.omni_verify_attention(*args) == -1
+    # rope: head_dim not a multiple of 8; nothing to do for zero tokens
+    rope = [FAKE, 3 * 4 * 12, FAKE, 8192, FAKE, None, None, FAKE, FAKE, FAKE, 1, 1, 1, 8, 64, 5, 4, 12, _lib.BF16, None]
+    assert lib.omni_rope_kv_append(*rope) == -3
+    rope[15] = 0
+    assert lib.omni_rope_kv_append(*rope) == 0
+    # propose: k = 0 and a window wider than the kernel's
+    reach = (ctypes.c_int32 * 8)(1, 1, 4, 2, 12, 4, 40, 6)
+    prop = [FAKE, 2048, 2048, FAKE, 1024, 1024, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 8, 0, 8, 64, 160, 256, 256, 3,
+            reach, None]
+    assert lib.omni_propose(*prop) == -3
+    prop[14] = 4
+    prop[18] = 8192
+    assert lib.omni_propose(*prop) == -3
+    # accept: 65 tokens per row; greedy_accept: an int dtype for the logits
+    acc = [FAKE, FAKE, FAKE, 2048, 2048, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 8, 65, 8188, 2, None]
+    assert lib.omni_accept(*acc) == -3
+    g = [FAKE, 10288, 10288, 5, FAKE, FAKE, FAKE, 2048, 2048, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 8, 5, 8188, 2, None]
+    assert lib.omni_greedy_accept(*g) == -2
+
+
+def test_kernels_refuse_without_gpu():
+    import torch
+
+    from omniasr_trt_amd import kernels
+
+    assert kernels.available(torch.device("cpu")) is False
+    with pytest.raises(Exception):
+        kernels.rope_kv(torch.zeros(1, 48), torch.zeros(8, 4, 2), torch.zeros(1, dtype=torch.long),
+                        torch.zeros(1, 4, 8, 8), torch.zeros(1, 4, 8, 8), 2)

@@ -1,0 +1,61 @@
+"""Host-side logic that needs no GPU: the reference's launch-split rule, module names of the decoder, constants."""
+
+import numpy as np
+import pytest
+import torch
+
+from omniasr_trt_amd import decode, kernels, llm, modeling, spec
+
+
+def test_splits_for_is_the_reference_rule():
+    # src/omniasr_trt/kernels.py:393-400: a power of two, about ``programs`` programs, 2 * block keys per split at least
+    assert kernels.splits_for(8, 32, 2560, 32, 264) == (1, 2560)
+    assert kernels.splits_for(8, 8, 2048, 64, 264) == (4, 512)
+    assert kernels.splits_for(1, 8, 256, 64, 264) == (4, 64)  # 264 // 8 = 33 wanted; 4 * 64 keys fill 256
+    assert kernels.splits_for(4, 8, 700, 32, 264) == (8, 96)
+
+
+def test_next_power_of_2():
+    assert [kernels.next_power_of_2(n) for n in (0, 1, 2, 3, 225, 256, 257)] == [1, 1, 2, 4, 256, 256, 512]
+
+
+def test_decoder_parameter_names_are_fairseq2s():
+    cfg = modeling.DecoderConfig(model_dim=32, num_layers=2, num_heads=2, ffn_dim=24, vocab_size=12, num_langs=5)
+    names = set(modeling.DecoderModel(cfg).state_dict())
+    want = {"text_frontend.weight", "final_proj.weight", "lang_embeddings.weight", "llama_decoder.layer_norm.weight"}
+    for i in range(2):
+        p = f"llama_decoder.layers.{i}."
+        want |= {p + "self_attn_layer_norm.weight", p + "ffn_layer_norm.weight"}
+        want |= {p + f"self_attn.{x}_proj.weight" for x in ("q", "k", "v", "output")}
+        want |= {p + f"ffn.{x}_proj.weight" for x in ("gate", "inner", "output")}
+    assert names == want
+
+
+def test_rope_table_follows_the_model_device_and_stays_fp32():
+    cfg = modeling.DecoderConfig(model_dim=32, num_layers=1, num_heads=2, ffn_dim=24, vocab_size=12, num_langs=5)
+    m = modeling.DecoderModel(cfg).to(torch.bfloat16)
+    assert m.rope.dtype == torch.float32 and m.rope.shape == (8192, 8, 2)
+    assert m.double().rope.dtype == torch.float32
+
+
+def test_reference_constants():
+    assert (spec.NGRAM, spec.BEHIND, spec.AHEAD, spec.SELF_WINDOW, spec.SELF_MIN) == (8, 64, 160, 256, 3)
+    assert spec.REACH == ((1, 1), (4, 2), (12, 4), (40, 6)) and spec.DRAFT_CAPACITY == 1024
+    assert decode.LIMIT == 8188 and decode.KEY_BUCKET == 256 and decode.CONTEXT_FLOOR == 2048
+    assert (llm.BOS, llm.PAD, llm.EOS) == (0, 1, 2)
+
+
+def test_row_draft():
+    frames = np.array([0, 0, 5, 5, 6, 0, 6, 7, 2, 7] * 100)
+    r = llm.Row(index=0, segments=2, frames=frames)
+    ids, before = r.draft(0)
+    assert before == 0 and ids[:6] == [5, 6, 6, 7, 7, 5]
+    assert llm.Row(index=1, segments=1).draft(0) is None
+
+
+def test_decoders_refuse_a_cpu_model():
+    cfg = modeling.DecoderConfig(model_dim=32, num_layers=1, num_heads=2, ffn_dim=24, vocab_size=12, num_langs=5)
+    with pytest.raises(RuntimeError):
+        decode.GreedyDecoder(modeling.DecoderModel(cfg))
+    with pytest.raises(ValueError):
+        decode.GreedyDecoder(modeling.DecoderModel(cfg), fused=False)

@@ -1,0 +1,369 @@
+"""The oracle pinned before it is trusted (CPU): golden vectors of the reference's own kernels, PyTorch's own ops on
+the same inputs, closed forms, invariants and brute force on tiny inputs."""
+
+from pathlib import Path
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import bf16
+from oracle import reference as oref
+from oracle import verify as ov
+
+GOLD = Path(__file__).parent / "golden"
+NGRAM, BEHIND, AHEAD, SELF_WINDOW, SELF_MIN = 8, 64, 160, 256, 3
+REACH = ((1, 1), (4, 2), (12, 4), (40, 6))
+W, SW = 256, 256  # pow2(BEHIND + AHEAD + 1), pow2(SELF_WINDOW)
+
+
+def _bf16_np(t: torch.Tensor) -> np.ndarray:
+    return t.float().numpy()
+
+
+# ---------------------------------------------------------------------------------------------- bf16
+
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal(200_000) * 10.0 ** rng.integers(-38, 38, 200_000)).astype(np.float32)
+    # exact ties (low half 0x8000) with even and odd upper halves, and the edges
+    ties = (np.arange(0x3F80, 0x3F80 + 512, dtype=np.uint32) << 16 | 0x8000).view(np.float32)
+    edges = np.array([0.0, -0.0, np.inf, -np.inf, 3.4e38, -3.4e38, 1e-40, -1e-40, 1.17e-38], dtype=np.float32)
+    x = np.concatenate([x, ties, edges])
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(bf16.to_bits(x), want)
+    assert bf16.to_bits(np.array([np.nan], dtype=np.float32))[0] == 0x7FC0
+
+
+# ---------------------------------------------------------------------------------------------- RoPE
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_rope_oracle_is_pytorchs_rounding(dtype):
+    """numpy's float32 evaluation order equals PyTorch's element-wise ``apply_rope`` bit for bit."""
+    g = torch.Generator().manual_seed(1)
+    n, h, d = 7, 4, 128
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    qkv = torch.randn(n, 3 * h * d, generator=g).to(tdt)
+    cs = oref.rope_table(d, 4096)
+    pos = torch.tensor([0, 1, 17, 999, 4095, 2048, 3])
+    kc = np.zeros((n, h, 4096, d), np.float32)
+    vc = np.zeros_like(kc)
+    q = ov.rope_kv(_bf16_np(qkv), cs.numpy(), pos.numpy(), kc, vc, h, dtype=dtype)
+    rq, rk, rv = qkv.view(n, 3, h, d).unbind(1)
+    c = cs[pos][:, None]
+    np.testing.assert_array_equal(q, oref.apply_rope(rq, c).float().numpy())
+    rows = np.arange(n)
+    np.testing.assert_array_equal(kc[rows, :, pos.numpy()], oref.apply_rope(rk, c).float().numpy())
+    np.testing.assert_array_equal(vc[rows, :, pos.numpy()], rv.float().numpy())
+
+
+def test_rope_table_closed_form():
+    """The product's fp32 table is the standard RoPE table: (cos, sin) of p * theta^(-2j/D), pairs interleaved."""
+    from omniasr_trt_amd import modeling
+
+    for d in (16, 128, 512):
+        cfg = modeling.DecoderConfig(model_dim=d * 2, num_heads=2)
+        t = modeling.rope_table(cfg).numpy().astype(np.float64)
+        ref = ov.rope_table(d, cfg.max_seq_len)
+        # fp32 angles p * inv lose up to ~p * 2^-24 rad: the bound grows with the position
+        err = np.abs(t - ref).max(axis=(1, 2))
+        bound = 1e-6 + np.arange(cfg.max_seq_len) * 2.0 ** -22
+        assert (err <= bound).all()
+        assert np.array_equal(t[0, :, 0], np.ones(d // 2)) and np.array_equal(t[0, :, 1], np.zeros(d // 2))
+
+
+def test_rope_rotation_properties():
+    """A rotation keeps each pair's norm, position 0 is the identity, and k/v land at (slot, head, position)."""
+    rng = np.random.default_rng(3)
+    n, h, d, s = 6, 3, 16, 40
+    qkv = rng.standard_normal((n, 3 * h * d)).astype(np.float32)
+    cs = ov.rope_table(d, s).astype(np.float32)
+    pos = np.array([0, 5, 39, 7, 0, 12])
+    slots = np.array([2, 0, 1, 2, 3, 1])
+    cache_pos = np.array([1, 2, 3, 4, 5, 6])
+    kc = np.full((4, h, s, d), 7.0, np.float32)
+    vc = np.full_like(kc, 7.0)
+    q = ov.rope_kv(qkv, cs, pos, kc, vc, h, slots, cache_pos, dtype="f32")
+    x = qkv.reshape(n, 3, h, d // 2, 2)
+    np.testing.assert_allclose(np.linalg.norm(q.reshape(n, h, d // 2, 2), axis=-1), np.linalg.norm(x[:, 0], axis=-1),
+                               rtol=1e-5)
+    np.testing.assert_array_equal(q[0], qkv.reshape(n, 3, h, d)[0, 0])  # angle 0
+    for i in range(n):
+        np.testing.assert_array_equal(vc[slots[i], :, cache_pos[i]], qkv.reshape(n, 3, h, d)[i, 2])
+    touched = np.zeros(kc.shape[:3], bool)
+    touched[slots, :, cache_pos] = True
+    assert (kc[~touched] == 7.0).all() and (vc[~touched] == 7.0).all()
+    # rotating by p then by r equals rotating by p + r (fp64 closed form)
+    t64 = ov.rope_table(d, 64)
+    a = x[1, 0].astype(np.float64)
+    z = a[..., 0] + 1j * a[..., 1]
+    rot = lambda z, p: z * (t64[p, :, 0] + 1j * t64[p, :, 1])  # noqa: E731
+    np.testing.assert_allclose(rot(rot(z, 5), 7), rot(z, 12), rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------------------------- attention
+
+def test_attention_oracle_is_the_textbook_formula():
+    rng = np.random.default_rng(4)
+    b, h, d, t, cap = 3, 2, 8, 4, 12
+    q = rng.standard_normal((b * t, h, d))
+    kc = rng.standard_normal((b + 1, h, cap, d))
+    vc = rng.standard_normal((b + 1, h, cap, d))
+    lengths = np.array([5, 0, 1])
+    out = ov.verify_attention(q, kc, vc, lengths, t, 0.3)
+    for r in range(b):
+        for i in range(t):
+            n = lengths[r] + i
+            for hh in range(h):
+                if n == 0:
+                    assert np.all(out[r * t + i, hh] == 0)
+                    continue
+                s = [0.3 * sum(q[r * t + i, hh, e] * kc[r, hh, j, e] for e in range(d)) for j in range(n)]
+                mx = max(s)
+                w = [math.exp(x - mx) for x in s]
+                o = [sum(w[j] * vc[r, hh, j, e] for j in range(n)) / sum(w) for e in range(d)]
+                np.testing.assert_allclose(out[r * t + i, hh], o, rtol=1e-12, atol=1e-12)
+
+
+def test_split_merge_identity():
+    """Split-K partials (m, l, acc) merged by log-sum-exp equal attention over all keys -- the kernels' merge."""
+    rng = np.random.default_rng(5)
+    n, d = 300, 16
+    q = rng.standard_normal(d)
+    k = rng.standard_normal((n, d))
+    v = rng.standard_normal((n, d))
+    s = k @ q * 0.25
+    full = (np.exp(s - s.max()) @ v) / np.exp(s - s.max()).sum()
+    parts = []
+    for lo, hi in ((0, 64), (64, 64), (64, 250), (250, 300)):  # one split empty
+        if hi == lo:
+            parts.append((-np.inf, 0.0, np.zeros(d)))
+            continue
+        m = s[lo:hi].max()
+        p = np.exp(s[lo:hi] - m)
+        parts.append((m, p.sum(), p @ v[lo:hi]))
+    top = max(m for m, _, _ in parts)
+    w = [0.0 if m == -np.inf else math.exp(m - top) for m, _, _ in parts]
+    merged = sum(wi * a for wi, (_, _, a) in zip(w, parts)) / sum(wi * l for wi, (_, l, _) in zip(w, parts))
+    np.testing.assert_allclose(merged, full, rtol=1e-12, atol=1e-12)
+
+
+def test_one_query_is_decode_attention():
+    rng = np.random.default_rng(6)
+    q = rng.standard_normal((3, 2, 8))
+    kc = rng.standard_normal((3, 2, 20, 8))
+    vc = rng.standard_normal((3, 2, 20, 8))
+    lengths = np.array([20, 1, 0])
+    out = ov.verify_attention(q, kc, vc, lengths, 1, 0.5)
+    for r, n in enumerate(lengths):
+        if n == 0:
+            assert np.all(out[r] == 0)
+            continue
+        ref = torch.softmax(torch.from_numpy(q[r])[:, None] @ torch.from_numpy(kc[r, :, :n]).transpose(-1, -2) * 0.5, -1)
+        np.testing.assert_allclose(out[r], (ref @ torch.from_numpy(vc[r, :, :n]))[:, 0].numpy(), rtol=1e-12)
+
+
+# ---------------------------------------------------------------------------------------------- argmax
+
+def test_argmax_oracle_matches_torch_log_softmax():
+    """The oracle's float32 log-probabilities against PyTorch's float32 ``F.log_softmax`` (CPU) to a few ulps, and its
+    bf16 argmax against the argmax of PyTorch's values rounded to bf16 -- equal on every row whose result does not
+    hinge on the last bits of the log-sum-exp."""
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(2000, 10288, generator=g).to(torch.bfloat16)
+    xn = _bf16_np(x)
+    ref = F.log_softmax(x.float(), -1).numpy()
+    y = ov.log_softmax_f32(xn)
+    assert np.abs(y - ref).max() <= 4 * np.spacing(np.float32(16.0))
+    want = bf16.round_bf16(ref).argmax(-1)
+    got = ov.log_softmax_argmax(xn, "bf16")
+    fragile = ov.argmax_is_fragile(xn, "bf16")
+    assert not ((got != want) & ~fragile).any()
+    assert fragile.mean() < 0.01
+    # the bucket rule matters: the plain argmax of the logits disagrees on about 1% of rows
+    assert 0.003 < (xn.argmax(-1) != got).mean() < 0.03
+
+
+def test_torch_cpu_bf16_log_softmax_is_another_rounding():
+    """PyTorch's CPU kernel for bf16 input keeps the sum and its log in bf16 (its buffers have the input's type):
+    y = bf16((x - m) - bf16(log(bf16(sum)))).  The reference runs the GPU kernel, which keeps them in fp32."""
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(200, 10288, generator=g).to(torch.bfloat16)
+    xn = _bf16_np(x)
+    m = xn.max(-1, keepdims=True)
+    s = np.exp(xn - m).astype(np.float32).sum(-1, keepdims=True, dtype=np.float64).astype(np.float32)
+    cpu_rule = bf16.round_bf16((xn - m) - bf16.round_bf16(np.log(bf16.round_bf16(s))))
+    np.testing.assert_array_equal(F.log_softmax(x, -1).float().numpy(), cpu_rule)
+
+
+def test_argmax_fp32_and_planted():
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(500, 37, generator=g)
+    np.testing.assert_array_equal(ov.log_softmax_argmax(x.numpy(), "f32"), F.log_softmax(x, -1).argmax(-1).numpy())
+    # config 1: a planted argmax 1.0 above the row maximum is the argmax whatever the rounding
+    y = torch.randn(5, 10288, generator=g).to(torch.bfloat16)
+    drafts = [11, 222, 3333, 4444]
+    for r in range(2):
+        y[r, drafts[r]] = y[r].float().max() + 1.0
+    got = ov.log_softmax_argmax(_bf16_np(y), "bf16")
+    assert got[0] == 11 and got[1] == 222
+
+
+# ---------------------------------------------------------------------------------------------- accept
+
+def test_accept_golden_vectors():
+    """The reference's own ``_accept`` (run under Triton's interpreter) on 24 random states."""
+    z = np.load(GOLD / "accept_golden.npz")
+    for c in range(int(z["cases"])):
+        p = f"c{c}_"
+        out, tok, last = z[p + "out"].copy(), z[p + "tok"].copy(), z[p + "last"].copy()
+        done, dn = z[p + "done"].copy(), z[p + "draft_next"].copy()
+        ov.accept(z[p + "tokens"], z[p + "nxt"], out, tok, last, done, dn, z[p + "start"], z[p + "use_draft"],
+                  int(z[p + "limit"]), int(z[p + "eos"]))
+        for name, got in (("out", out), ("tok", tok), ("last", last), ("done", done), ("draft_next", dn)):
+            np.testing.assert_array_equal(got, z[p + name + "_after"], err_msg=f"case {c} {name}")
+
+
+def test_accept_known_answers():
+    """Planted: the first two drafts match -> n = 2, three tokens kept, last += 3; EOS and the limit cut a step."""
+    t0, d = 9, [5, 6, 7, 8]
+    tokens = np.array([[t0] + d] * 3)
+    nxt = np.array([[5, 6, 4, 8, 3], [5, 2, 7, 8, 3], [5, 6, 7, 8, 3]])
+    out = np.full((3, 64), 1, np.int32)
+    tok, last = np.array([t0] * 3), np.array([10, 20, 30])
+    done = np.zeros(3, bool)
+    dn, start, use = np.array([100, 100, 100]), np.array([50, 50, 50]), np.array([True, False, True])
+    ov.accept(tokens, nxt, out, tok, last, done, dn, start, use, limit=33, eos=2)
+    assert list(out[0, 11:14]) == [5, 6, 4] and last[0] == 13 and tok[0] == 4 and not done[0] and dn[0] == 53
+    assert list(out[1, 21:23]) == [5, 2] and last[1] == 22 and tok[1] == 2 and done[1] and dn[1] == 102
+    # row 2: everything matches, but position 31 + 2 = 33 >= limit stops at j = 2
+    assert list(out[2, 31:34]) == [5, 6, 7] and last[2] == 33 and done[2] and dn[2] == 53
+
+
+def test_accept_one_token_is_the_greedy_update():
+    rng = np.random.default_rng(9)
+    for _ in range(50):
+        b = 12
+        nxt = rng.integers(0, 6, b)
+        last = rng.integers(0, 60, b)
+        done = rng.random(b) < 0.3
+        out = rng.integers(3, 9, (b, 64)).astype(np.int32)
+        tok = rng.integers(3, 9, b)
+        a = [x.copy() for x in (out, tok, last, done)]
+        ov.accept(tok[:, None], nxt[:, None], a[0], a[1], a[2], a[3], None, None, None, limit=40, eos=2)
+        g = [x.copy() for x in (out, tok, last, done)]
+        ov.greedy_update(nxt, g[0], g[1], g[2], g[3], limit=40, eos=2)
+        for x, y in zip(a, g):
+            np.testing.assert_array_equal(x, y)
+
+
+# ---------------------------------------------------------------------------------------------- propose
+
+def test_propose_golden_vectors():
+    """The reference's ``_propose`` kernel and ``reference_propose`` (which agreed) on 12 trials."""
+    z = np.load(GOLD / "propose_golden.npz")
+    const = z["constants"]
+    assert list(const[:5]) == [NGRAM, BEHIND, AHEAD, SELF_WINDOW, SELF_MIN]
+    assert [tuple(const[5 + 2 * i: 7 + 2 * i]) for i in range(4)] == list(REACH)
+    for t in range(int(z["trials"])):
+        p = f"t{t}_"
+        prop, use, start = ov.propose(z[p + "out"], z[p + "draft"], z[p + "draft_len"], z[p + "last"], z[p + "first"],
+                                      z[p + "next"], int(z[p + "k"]), NGRAM, BEHIND, AHEAD, REACH, W, SW, SELF_MIN)
+        np.testing.assert_array_equal(prop, z[p + "prop"], err_msg=f"trial {t}")
+        np.testing.assert_array_equal(use, z[p + "use_draft"], err_msg=f"trial {t}")
+        np.testing.assert_array_equal(start, z[p + "start"], err_msg=f"trial {t}")
+
+
+def _tiny_propose_case(rng, b=6, cap=80, dcap=60, vocab=4):
+    out = rng.integers(3, 3 + vocab, (b, cap)).astype(np.int32)
+    first = rng.integers(0, 20, b)
+    last = np.minimum(first + rng.integers(0, 50, b), cap - 1)
+    out[np.arange(cap)[None, :] < first[:, None]] = 1
+    dlen = rng.integers(0, dcap + 1, b)
+    draft = rng.integers(3, 3 + vocab, (b, dcap)).astype(np.int32)
+    draft[np.arange(dcap)[None, :] >= dlen[:, None]] = -1
+    nxt = (rng.random(b) * (dlen + 6)).astype(np.int64)
+    return out, draft, dlen, last, first, nxt
+
+
+def test_propose_brute_force():
+    rng = np.random.default_rng(10)
+    for trial in range(60):
+        case = _tiny_propose_case(rng, vocab=2 + trial % 4)
+        k, ngram = 1 + trial % 5, 2 + trial % 6
+        behind, ahead = 3 + trial % 7, 5 + trial % 9
+        width = 1 << (behind + ahead).bit_length()
+        reach = ((0, 1), (2, 2), (4, 3), (6, 4))
+        a = ov.propose(*case, k, ngram, behind, ahead, reach, width, 16, 2)
+        b = ov.propose_loops(*case, k, ngram, behind, ahead, reach, width, 16, 2)
+        for x, y in zip(a, b):
+            np.testing.assert_array_equal(x, y, err_msg=f"trial {trial}")
+
+
+def test_propose_invariants():
+    # a perfect draft: the generated tokens are the draft's first tokens -> propose the next ones from the draft
+    draft_tokens = list(range(10, 60))
+    out = np.full((1, 128), 1, np.int32)
+    first, last = 20, 29  # 10 generated tokens = draft[0..9]
+    out[0, first:last + 1] = draft_tokens[:10]
+    draft = np.full((1, 64), -1, np.int32)
+    draft[0, :50] = draft_tokens
+    prop, use, start = ov.propose(out, draft, np.array([50]), np.array([last]), np.array([first]), np.array([10]),
+                                  4, NGRAM, BEHIND, AHEAD, REACH, W, SW, SELF_MIN)
+    assert use[0] and list(prop[0]) == draft_tokens[10:14] and start[0] == 10
+    # a repetition loop and no draft: continue with the period
+    out = np.full((1, 128), 1, np.int32)
+    loop = [7, 8, 9] * 10
+    out[0, 0:30] = loop
+    prop, use, _ = ov.propose(out, np.full((1, 8), -1, np.int32), np.array([0]), np.array([29]), np.array([0]),
+                              np.array([0]), 5, NGRAM, BEHIND, AHEAD, REACH, W, SW, SELF_MIN)
+    assert not use[0] and list(prop[0]) == [7, 8, 9, 7, 8]
+
+
+def test_spec_prepare_rules():
+    rng = np.random.default_rng(11)
+    out, draft, dlen, last, first, nxt = _tiny_propose_case(rng, b=5)
+    tok = rng.integers(3, 7, 5)
+    done = np.array([False, True, False, True, False])
+    tokens, pos, slots, lengths, use, start = ov.spec_prepare(out, draft, dlen, last, first, nxt, tok, done, 60, 3,
+                                                              NGRAM, 4, 6, REACH, 16, 16, 2)
+    prop, use2, start2 = ov.propose(out, draft, dlen, last, first, nxt, 3, NGRAM, 4, 6, REACH, 16, 16, 2)
+    np.testing.assert_array_equal(tokens[:, 0], tok)
+    np.testing.assert_array_equal(tokens[:, 1:], prop)
+    for b in range(5):
+        want = [min(last[b], 59)] * 4 if done[b] else [min(last[b] + 1 + j, 59) for j in range(4)]
+        assert list(pos[b * 4:(b + 1) * 4]) == want
+        assert lengths[b] == (0 if done[b] else last[b] + 2)
+    np.testing.assert_array_equal(slots, np.repeat(np.arange(5), 4))
+
+
+# ---------------------------------------------------------------------------------------------- drafts, host rules
+
+def test_frames_to_draft_matches_loop():
+    from omniasr_trt_amd import llm
+
+    rng = np.random.default_rng(12)
+    for trial in range(40):
+        frames = rng.integers(0, 6, rng.integers(0, 400))
+        seg_samples = 2000 + 320 * int(rng.integers(0, 5))
+        for seg in range(3):
+            assert llm.frames_to_draft(frames, seg, seg_samples) == ov.frames_to_draft(frames, seg, seg_samples)
+    # hand-computed: segment 1 of 6400-sample segments is frames [20, 40), window [0, 90) -> 25 frames before
+    frames = np.array([0] * 5 + [3, 3, 4, 0, 4] + [5] * 15 + [6, 2, 6] + [7] * 10)
+    ids, before = llm.frames_to_draft(frames, 1, 6400)
+    assert ids == [3, 4, 4, 5, 6, 6, 7] and before == 4
+
+
+def test_early_stop_rule_known_answers():
+    from omniasr_trt_amd import llm
+
+    out = np.full(1000, 1, dtype=np.int32)
+    out[300:] = 7
+    assert llm.compression_ratio(out[400:500]) > 4.0
+    assert llm.compression_ratio(out[400:500]) == oref.compression_ratio(out[400:500])
+    assert llm.early_stop_index(out, 240, 600, ctx=300) == 500
+    assert llm.early_stop_index(out, 240, 499, ctx=300) is None
+    assert llm.early_stop_index(out, 240, 800, ctx=420) == 750
