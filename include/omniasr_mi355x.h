@@ -91,7 +91,8 @@ size_t omni_verify_attention_workspace(int32_t rows, int32_t tokens, int32_t hea
  * ``cache_len`` positions): out = softmax(q.k * scale) . v, accumulated in fp32; an empty key range
  * gives zeros.  All keys must lie within the first ``keys`` positions (the graph bucket); the launch
  * grid depends on ``keys`` only.  One pass over a row's keys serves all of its queries.
- * ``chunk``: keys per split (a multiple of 32; 0: omni_verify_attention_chunk()).
+ * ``chunk``: keys per split (a multiple of 32; 0: omni_verify_attention_chunk()); a row with n keys has
+ * ceil(n / chunk) splits, and its 32-key tiles are dealt out round-robin over them.
  * ``workspace``: at least omni_verify_attention_workspace() bytes, 256-byte aligned, any content.
  * ``counters``: rows*heads int32, zero before the first call; every call leaves them zero (calls
  * that share them must not overlap in time).

@@ -50,8 +50,9 @@ struct AttnArgs {
 
 struct SplitRange {
   int64_t n;      // keys every query of the row sees (lengths[b], clamped to the cache)
-  int64_t stop;   // end of this split's keys
-  int64_t start;  // first key of this split
+  int64_t total;  // keys the row's last query sees (clamped to the cache and the grid)
+  int64_t stop;   // end of this split's keys (contiguous ranges)
+  int64_t start;  // first key of this split (contiguous ranges)
   int nact;       // splits holding keys of this row (>= 1: an empty row still writes zeros)
 };
 
@@ -62,6 +63,7 @@ __device__ __forceinline__ SplitRange split_range(const AttnArgs& a, int b, int 
   total = total < a.cache_len ? total : a.cache_len;
   const int64_t covered = (int64_t)a.splits * a.chunk;
   total = total < covered ? total : covered;
+  r.total = total;
   int64_t nact = ceil_div64(total, a.chunk);
   r.nact = (int)(nact < 1 ? 1 : nact);
   r.start = (int64_t)sp * a.chunk;
@@ -99,7 +101,7 @@ __device__ void merge_splits(const AttnArgs& a, int b, int h, int nact) {
     float den = 0.f;
     for (int s = lane; s < nact; s += kWave) {
       const float m = a.part_ml[((split0 + s) * a.T + t) * 2];
-      const float w = m == -INFINITY ? 0.f : exp2f(m - top);
+      const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - top);
       den += w * a.part_ml[((split0 + s) * a.T + t) * 2 + 1];
     }
     den = wave_sum(den);
@@ -109,7 +111,7 @@ __device__ void merge_splits(const AttnArgs& a, int b, int h, int nact) {
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
       for (int s = 0; s < nact; ++s) {
         const float m = a.part_ml[((split0 + s) * a.T + t) * 2];
-        const float w = m == -INFINITY ? 0.f : exp2f(m - top);
+        const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - top);
         const f32x4_t po = *reinterpret_cast<const f32x4_t*>(a.part_o + ((split0 + s) * a.T + t) * a.D + d);
         acc += w * po;
       }
@@ -136,8 +138,195 @@ __device__ __forceinline__ void finish_split(const AttnArgs& a, int b, int h, in
 
 // ---------------------------------------------------------------------------------------------- MFMA
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Scores are kept relative to a reference max m_ref (log2 domain) that only moves when a score exceeds it by
+// more than 2^kLazyLog2: the cross-lane max and the rescale of O are skipped for almost every tile, and
+// probabilities stay <= 2^kLazyLog2 (exact in fp32, and bf16 keeps its relative precision at any scale).
+constexpr float kLazyLog2 = 8.0f;
+
+// One 32-key tile of K and V in MFMA operand layout (see the file comment).
 template <int D>
-__global__ __launch_bounds__(64) void verify_attn_mfma_kernel(AttnArgs a) {
+struct KVTile {
+  static constexpr int KS = D / 32, NG = D / 128;
+  u32x4_t k[2][KS];
+  u32x4_t v[NG][8];
+};
+
+// Per-lane byte offsets of a tile's elements from the tile's first key (constant over the loop).
+struct TileOffsets {
+  uint32_t k0, k1;   // K rows of MFMA blocks 0 and 1
+  uint32_t v[8];     // V rows kb + 8g + j
+};
+
+__device__ __forceinline__ u32x4_t ld16(const char* p) { return *reinterpret_cast<const u32x4_t*>(p); }
+
+// A full tile: the wave-uniform tile base (scalar registers) plus the lane's constant offsets.
+template <int D>
+__device__ __forceinline__ void load_tile(KVTile<D>& t, const char* kt, const char* vt, const TileOffsets& o) {
+#pragma unroll
+  for (int s = 0; s < KVTile<D>::KS; ++s) {
+    t.k[0][s] = ld16(kt + o.k0 + s * 64);
+    t.k[1][s] = ld16(kt + o.k1 + s * 64);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+#pragma unroll
+    for (int gg = 0; gg < KVTile<D>::NG; ++gg) t.v[gg][j] = ld16(vt + o.v[j] + gg * 256);
+  }
+}
+
+// The last tile of a split: keys past the cache end are read at the last position and V past ``stop`` is zeroed
+// (0 * anything stays 0 in the PV product; those keys are masked out of the softmax).
+template <int D>
+__device__ __forceinline__ void load_tail_tile(KVTile<D>& t, const uint16_t* kbase, const uint16_t* vbase,
+                                               int64_t kb, int64_t stop, int64_t last_key, int64_t s_pos, int c,
+                                               int g) {
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+    int64_t key = kb + 8 * (c >> 2) + 4 * mb + (c & 3);
+    key = key < last_key ? key : last_key;
+    const uint16_t* kp = kbase + key * s_pos + g * 8;
+#pragma unroll
+    for (int s = 0; s < KVTile<D>::KS; ++s) t.k[mb][s] = *reinterpret_cast<const u32x4_t*>(kp + s * 32);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int64_t key = kb + 8 * g + j;
+    const int64_t kl = key < last_key ? key : last_key;
+    const uint16_t* vp = vbase + kl * s_pos + c * 8;
+#pragma unroll
+    for (int gg = 0; gg < KVTile<D>::NG; ++gg)
+      t.v[gg][j] = key < stop ? *reinterpret_cast<const u32x4_t*>(vp + gg * 128) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+}
+
+// S^T for the tile: lane (c, g) gets query c's raw scores for keys kb + 8g + j, j = 0..7.
+template <int D>
+__device__ __forceinline__ void tile_scores(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float (&sv)[8]) {
+  f32x4_t sacc[2];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+    sacc[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s)
+      sacc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, t.k[mb][s]),
+                                                         __builtin_bit_cast(bf16x8_t, qop[s]), sacc[mb], 0, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sv[j] = sacc[j >> 2][j & 3];
+}
+
+// Move the reference max of every row to ``m_new`` (rows 4g + i of O live in this lane; their alphas in lanes
+// 4g + i), rescaling O and this lane's share of the probability sum.
+template <int NB>
+__device__ __forceinline__ void rescale(float m_old, float m_new_use, float& l_run, f32x4_t (&o)[NB], int g) {
+  const float alpha = __builtin_amdgcn_exp2f(m_old - m_new_use);  // m_old = -inf: 0
+  l_run *= alpha;
+  float al[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * g + i, kWave);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[nb][i] *= al[i];
+  }
+}
+
+// O += P V for the tile: P from this lane's 8 probabilities (its A operand), V transposed in registers.
+template <int D>
+__device__ __forceinline__ void tile_pv(const KVTile<D>& t, const float (&p)[8], f32x4_t (&o)[D / 16]) {
+  u32x4_t pop;
+#pragma unroll
+  for (int w = 0; w < 4; ++w)
+    pop[w] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{p[2 * w], p[2 * w + 1]}), bf16x2_t));
+#pragma unroll
+  for (int gg = 0; gg < D / 128; ++gg) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      u32x4_t bop;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t lo = t.v[gg][2 * w][e >> 1];
+        const uint32_t hi = t.v[gg][2 * w + 1][e >> 1];
+        // element e of rows 2w and 2w+1: one byte permute
+        bop[w] = __builtin_amdgcn_perm(hi, lo, (e & 1) ? 0x07060302u : 0x05040100u);
+      }
+      o[gg * 8 + e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pop),
+                                                              __builtin_bit_cast(bf16x8_t, bop), o[gg * 8 + e], 0,
+                                                              0, 0);
+    }
+  }
+}
+
+struct SoftmaxState {
+  float m_ref;  // reference max of query c (log2 domain), equal over g
+  float thr;    // raw-score threshold above which m_ref must move
+  float l_run;  // this lane's share of query c's probability sum (relative to m_ref)
+};
+
+// A tile every query sees entirely: lazy reference max.
+template <int D>
+__device__ __forceinline__ void attend_full(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float c_scale,
+                                            SoftmaxState& st, f32x4_t (&o)[D / 16], int g) {
+  float sv[8];
+  tile_scores<D>(t, qop, sv);
+  bool over = false;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) over |= sv[j] > st.thr;
+  if (__any(over)) {
+    float mx = sv[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sv[j]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float m_new = fmaxf(st.m_ref, mx * c_scale);
+    rescale<D / 16>(st.m_ref, m_new, st.l_run, o, g);
+    st.m_ref = m_new;
+    st.thr = (m_new + kLazyLog2) / c_scale;
+  }
+  float p[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], c_scale, -st.m_ref));
+    st.l_run += p[j];
+  }
+  tile_pv<D>(t, p, o);
+}
+
+// A tile reaching past some query's last key or the split's end: exact max over the visible keys.
+template <int D>
+__device__ __forceinline__ void attend_masked(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float c_scale,
+                                              SoftmaxState& st, f32x4_t (&o)[D / 16], int g, int64_t key0,
+                                              int64_t lim) {
+  float sv[8];
+  tile_scores<D>(t, qop, sv);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (key0 + j >= lim) sv[j] = -INFINITY;
+  float mx = sv[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sv[j]);
+  mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+  const float m_new = fmaxf(st.m_ref, mx * c_scale);
+  const float m_use = m_new == -INFINITY ? 0.f : m_new;
+  rescale<D / 16>(st.m_ref, m_use, st.l_run, o, g);
+  st.m_ref = m_new;
+  st.thr = m_new == -INFINITY ? -INFINITY : (m_new + kLazyLog2) / c_scale;
+  float p[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], c_scale, -m_use));
+    st.l_run += p[j];
+  }
+  tile_pv<D>(t, p, o);
+}
+
+// PIPE: the next tile's loads are issued before the current tile's math (two tiles of registers).
+template <int D, bool PIPE>
+__global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(AttnArgs a) {
   constexpr int KS = D / 32;  // k-steps of S^T = K Q^T
   constexpr int NG = D / 128;  // 128-wide output groups
   const int sp = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -149,6 +338,7 @@ __global__ __launch_bounds__(64) void verify_attn_mfma_kernel(AttnArgs a) {
   const uint16_t* kbase = reinterpret_cast<const uint16_t*>(a.k) + b * a.s_row + h * a.s_head;
   const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.v) + b * a.s_row + h * a.s_head;
   const int64_t last_key = a.cache_len - 1;
+  const float c_scale = a.scale_log2;
 
   // B operand of S^T = K Q^T: lane (c, g) holds q[c][32s + 8g .. 32s + 8g + 7].
   u32x4_t qop[KS];
@@ -160,115 +350,65 @@ __global__ __launch_bounds__(64) void verify_attn_mfma_kernel(AttnArgs a) {
     for (int s = 0; s < KS; ++s) qop[s] = c < T ? *reinterpret_cast<const u32x4_t*>(qrow + s * 32) : zero;
   }
 
-  float m_run = -INFINITY;  // running max of query c (log2 domain), equal over g
-  float l_run = 0.f;        // this lane's share of query c's sum of probabilities
-  f32x4_t o[NG * 8];        // o[8gg + e][i]: output row 4g + i, dimension 128gg + 8c + e
+  SoftmaxState st{-INFINITY, -INFINITY, 0.f};
+  f32x4_t o[NG * 8];  // o[8gg + e][i]: output row 4g + i, dimension 128gg + 8c + e
 #pragma unroll
   for (int nb = 0; nb < NG * 8; ++nb) o[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int64_t see_all = r.stop < r.n ? r.stop : r.n;  // keys below this are seen by every query
-  const int64_t lim_c = (r.n + c) < r.stop ? (r.n + c) : r.stop;  // query c's key limit here
+  // The row's 32-key tiles are dealt out round-robin over its nact splits: split sp takes tiles sp, sp + nact,
+  // sp + 2 nact, ...  Each split gets the same number of tiles (give or take one), and at any moment the row's
+  // splits read neighbouring tiles (DRAM locality), unlike contiguous per-split ranges.  Tiles below
+  // min(total, n) are seen whole by every query: no masks, no clamps.
+  const int64_t row_tiles = (r.total + 31) >> 5;
+  const int64_t see_all = r.total < r.n ? r.total : r.n;
+  const int64_t full_tiles = see_all >> 5;  // tiles [0, full_tiles) are full
+  const int64_t nfull = full_tiles > sp ? (full_tiles - sp + r.nact - 1) / r.nact : 0;
+  const uint32_t pos_bytes = (uint32_t)(a.s_pos * 2);
+  TileOffsets off;
+  off.k0 = (uint32_t)(8 * (c >> 2) + (c & 3)) * pos_bytes + g * 16;
+  off.k1 = off.k0 + 4 * pos_bytes;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) off.v[j] = (uint32_t)(8 * g + j) * pos_bytes + c * 16;
+  const char* kt = reinterpret_cast<const char*>(kbase) + (int64_t)sp * 32 * a.s_pos * 2;
+  const char* vt = reinterpret_cast<const char*>(vbase) + (int64_t)sp * 32 * a.s_pos * 2;
+  const int64_t tile_bytes = (int64_t)r.nact * 32 * a.s_pos * 2;  // stride between this split's tiles
 
-  for (int64_t kb = r.start; kb < r.stop; kb += 32) {
-    // ---- S^T for 32 keys: two 16-key MFMA blocks
-    f32x4_t sacc[2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      int64_t key = kb + 8 * (c >> 2) + 4 * mb + (c & 3);
-      key = key < last_key ? key : last_key;
-      const uint16_t* kp = kbase + key * a.s_pos + g * 8;
-      u32x4_t kr[KS];
-#pragma unroll
-      for (int s = 0; s < KS; ++s) kr[s] = *reinterpret_cast<const u32x4_t*>(kp + s * 32);
-      sacc[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-        sacc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[s]),
-                                                           __builtin_bit_cast(bf16x8_t, qop[s]),
-                                                           sacc[mb], 0, 0, 0);
-    }
-    // ---- V rows kb + 8g + j, dimensions 128gg + 8c .. +7
-    u32x4_t vr[NG][8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      int64_t key = kb + 8 * g + j;
-      key = key < last_key ? key : last_key;
-      const uint16_t* vp = vbase + key * a.s_pos + c * 8;
-#pragma unroll
-      for (int gg = 0; gg < NG; ++gg) vr[gg][j] = *reinterpret_cast<const u32x4_t*>(vp + gg * 128);
-    }
-
-    float sv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sv[j] = sacc[j >> 2][j & 3] * a.scale_log2;
-    if (kb + 32 > see_all) {  // the tile reaches past some query's keys or the split's end
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int64_t key = kb + 8 * g + j;
-        if (key >= lim_c) sv[j] = -INFINITY;
-        if (key >= r.stop) {  // not a key of this row: zero V so that 0 * garbage stays 0
-#pragma unroll
-          for (int gg = 0; gg < NG; ++gg) vr[gg][j] = u32x4_t{0u, 0u, 0u, 0u};
-        }
+  KVTile<D> A;
+  if constexpr (PIPE) {
+    KVTile<D> B;
+    if (nfull > 0) load_tile<D>(A, kt, vt, off);
+    for (int64_t i = 0; i < nfull; i += 2) {
+      if (i + 1 < nfull) load_tile<D>(B, kt + tile_bytes, vt + tile_bytes, off);
+      attend_full<D>(A, qop, c_scale, st, o, g);
+      if (i + 1 < nfull) {
+        if (i + 2 < nfull) load_tile<D>(A, kt + 2 * tile_bytes, vt + 2 * tile_bytes, off);
+        attend_full<D>(B, qop, c_scale, st, o, g);
       }
+      kt += 2 * tile_bytes;
+      vt += 2 * tile_bytes;
     }
-    float mx = sv[0];
-#pragma unroll
-    for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sv[j]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    float p[8];
-    float psum = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      p[j] = exp2f(sv[j] - m_use);
-      psum += p[j];
+  } else {
+    for (int64_t i = 0; i < nfull; ++i) {
+      load_tile<D>(A, kt, vt, off);
+      attend_full<D>(A, qop, c_scale, st, o, g);
+      kt += tile_bytes;
+      vt += tile_bytes;
     }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    u32x4_t pop;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) pop[w] = pack_bf16x2(p[2 * w], p[2 * w + 1]);
-
-    // rescale the output rows this lane holds (rows 4g + i live in lanes c = 4g + i)
-    float al[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * g + i, kWave);
-#pragma unroll
-    for (int nb = 0; nb < NG * 8; ++nb) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[nb][i] *= al[i];
-    }
-
-    // ---- O += P V: B operand (gg, e) = element e of vr[gg][0..7]
-#pragma unroll
-    for (int gg = 0; gg < NG; ++gg) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        u32x4_t bop;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const uint32_t lo = vr[gg][2 * w][e >> 1];
-          const uint32_t hi = vr[gg][2 * w + 1][e >> 1];
-          bop[w] = (e & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-        }
-        o[gg * 8 + e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pop),
-                                                                __builtin_bit_cast(bf16x8_t, bop),
-                                                                o[gg * 8 + e], 0, 0, 0);
-      }
-    }
+  }
+  const int64_t lim_c = (r.n + c) < r.total ? (r.n + c) : r.total;  // query c's key limit
+  for (int64_t ti = sp + nfull * r.nact; ti < row_tiles; ti += r.nact) {  // the row's last one or two tiles
+    const int64_t kb = ti * 32;
+    load_tail_tile<D>(A, kbase, vbase, kb, r.total, last_key, a.s_pos, c, g);
+    attend_masked<D>(A, qop, c_scale, st, o, g, kb + 8 * g, lim_c);
   }
 
   // ---- finish: per-query sums, then either the output or this split's partial
-  float l_tot = l_run + __shfl_xor(l_run, 16, kWave);
+  float l_tot = st.l_run + __shfl_xor(st.l_run, 16, kWave);
   l_tot += __shfl_xor(l_tot, 32, kWave);
   float li[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) li[i] = __shfl(l_tot, 4 * g + i, kWave);
-  if (r.nact == 1 && !a.separate) {
+  if (r.nact == 1) {
     uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -298,7 +438,7 @@ __global__ __launch_bounds__(64) void verify_attn_mfma_kernel(AttnArgs a) {
     }
   }
   if (g == 0 && c < T) {
-    a.part_ml[(base + c) * 2] = m_run;
+    a.part_ml[(base + c) * 2] = st.m_ref;
     a.part_ml[(base + c) * 2 + 1] = l_tot;
   }
   finish_split<uint16_t>(a, b, h, r.nact);
@@ -390,7 +530,7 @@ __global__ __launch_bounds__(64) void verify_attn_valu_kernel(AttnArgs a) {
     __syncthreads();
   }
 
-  const bool direct = r.nact == 1 && !a.separate;
+  const bool direct = r.nact == 1;
   const int64_t base = (((int64_t)b * a.H + h) * a.splits + sp) * T;
   Elem* out = reinterpret_cast<Elem*>(a.out);
 #pragma unroll
@@ -423,11 +563,64 @@ __global__ __launch_bounds__(64) void verify_attn_valu_kernel(AttnArgs a) {
 
 // ---------------------------------------------------------------------------------------------- combine
 
-template <typename OutT>
+// Second launch of the split merge: one wave per (query row t, head, row b), every load issued at once (one
+// memory round trip).  Lane s holds split s's (m, l); each lane keeps D/64 output dimensions of every split.
+constexpr int kCombineMaxSplits = 32;
+
+template <typename OutT, int DPL>
 __global__ __launch_bounds__(64) void verify_attn_combine_kernel(AttnArgs a) {
-  const int h = blockIdx.x, b = blockIdx.y;
+  const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const SplitRange r = split_range(a, b, 0);
-  merge_splits<OutT>(a, b, h, r.nact);
+  const int nact = r.nact;
+  if (nact == 1) return;  // written directly by its only split
+  const int lane = threadIdx.x;
+  const int T = a.T, D = a.D;
+  const int64_t split0 = ((int64_t)b * a.H + h) * a.splits;
+  OutT* orow = reinterpret_cast<OutT*>(a.out) + ((int64_t)(b * T + t) * a.H + h) * D;
+  if (nact > kCombineMaxSplits) {  // beyond the unrolled case: the generic merge
+    if (t == 0) merge_splits<OutT>(a, b, h, nact);
+    return;
+  }
+  const int d0 = lane * DPL;
+  const bool has_d = d0 < D;
+  float po[kCombineMaxSplits][DPL];
+#pragma unroll
+  for (int s = 0; s < kCombineMaxSplits; ++s) {
+    if (s < nact && has_d) {
+      const float* src = a.part_o + ((split0 + s) * T + t) * D + d0;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) po[s][e] = src[e];
+    }
+  }
+  float m = -INFINITY, l = 0.f;
+  if (lane < nact) {
+    m = a.part_ml[((split0 + lane) * T + t) * 2];
+    l = a.part_ml[((split0 + lane) * T + t) * 2 + 1];
+  }
+  const float top = wave_max(m);
+  const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - top);
+  const float den = wave_sum(w * l);
+  const float div = den > 0.f ? den : 1.f;
+  float acc[DPL];
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+#pragma unroll
+  for (int s = 0; s < kCombineMaxSplits; ++s) {
+    if (s < nact) {
+      const float ws = __shfl(w, s, kWave);
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) acc[e] += ws * po[s][e];
+    }
+  }
+  if (!has_d) return;
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) {
+    const float v = acc[e] / div;
+    if constexpr (sizeof(OutT) == 2)
+      orow[d0 + e] = (uint16_t)f32_to_bf16_rne(v);
+    else
+      orow[d0 + e] = v;
+  }
 }
 
 }  // namespace omni
@@ -441,15 +634,14 @@ extern "C" int32_t omni_verify_attention_chunk(int32_t rows, int32_t tokens, int
   (void)tokens;
   (void)head_dim;
   if (rows <= 0 || heads <= 0 || keys <= 0) return 64;
-  // About 2048 waves over the chip's 256 CUs (8 per CU) when the rows are full, at least 64 keys
-  // per split so that a wave's fixed cost (its queries, its partial) stays small.
+  // About 2048 waves (8 per CU) when the rows are full, at most 8 tiles (256 keys) per split: measured on
+  // config 3 (8 rows x 32 heads, 750-2400 keys), 224-256 keys per split are among the fastest and longer
+  // splits leave too few waves in flight; at least 64 keys so that a split's fixed cost stays small.
   const int64_t items = (int64_t)rows * heads;
-  int64_t want = (2048 + items - 1) / items;
-  int64_t chunk = (keys + want - 1) / want;
-  chunk = (chunk + 63) / 64 * 64;
+  int64_t chunk = ((int64_t)keys * items + 2047) / 2048;
+  chunk = (chunk + 31) / 32 * 32;
+  if (chunk > 256) chunk = 256;
   if (chunk < 64) chunk = 64;
-  const int64_t whole = ((int64_t)keys + 31) / 32 * 32;
-  if (chunk > whole) chunk = whole;
   return (int32_t)chunk;
 }
 
@@ -472,13 +664,14 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
                                      size_t workspace_bytes, int32_t* counters, int32_t flags,
                                      int32_t dtype, void* stream) {
   if (rows < 0 || heads <= 0 || head_dim <= 0 || keys <= 0 || cache_len <= 0) return OMNI_ERR_INVALID;
+  if (!(scale > 0.f)) return OMNI_ERR_INVALID;  // a softmax scale is positive (head_dim^-1/2)
   if (rows == 0) return OMNI_OK;
   if (!q || !k_cache || !v_cache || !lengths || !out || !workspace || !counters) return OMNI_ERR_INVALID;
   if (tokens < 1 || tokens > 16) return OMNI_ERR_SHAPE;
   if (dtype != OMNI_BF16 && dtype != OMNI_F32) return OMNI_ERR_DTYPE;
   if (head_dim % 8 != 0 || head_dim > kValuMaxD) return OMNI_ERR_SHAPE;
   if (chunk == 0) chunk = omni_verify_attention_chunk(rows, tokens, heads, head_dim, keys);
-  if (chunk <= 0 || chunk % 64 != 0) return OMNI_ERR_INVALID;
+  if (chunk <= 0 || chunk % 32 != 0) return OMNI_ERR_INVALID;
   if (workspace_bytes < omni_verify_attention_workspace(rows, tokens, heads, head_dim, keys, chunk))
     return OMNI_ERR_WORKSPACE;
   if (((uintptr_t)workspace & 255u) != 0) return OMNI_ERR_WORKSPACE;
@@ -515,9 +708,9 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
   dim3 grid(splits, heads, rows);
   if (mfma) {
     switch (head_dim) {
-      case 128: verify_attn_mfma_kernel<128><<<grid, 64, 0, s>>>(a); break;
-      case 256: verify_attn_mfma_kernel<256><<<grid, 64, 0, s>>>(a); break;
-      case 512: verify_attn_mfma_kernel<512><<<grid, 64, 0, s>>>(a); break;
+      case 128: verify_attn_mfma_kernel<128, true><<<grid, 64, 0, s>>>(a); break;
+      case 256: verify_attn_mfma_kernel<256, false><<<grid, 64, 0, s>>>(a); break;
+      case 512: verify_attn_mfma_kernel<512, false><<<grid, 64, 0, s>>>(a); break;
       default: verify_attn_valu_kernel<uint16_t><<<grid, 64, 0, s>>>(a); break;
     }
   } else if (dtype == OMNI_BF16) {
@@ -527,8 +720,20 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
   }
   int st = omni_launch_status();
   if (st != OMNI_OK || !a.separate) return st;
-  dim3 cgrid(heads, rows);
-  if (dtype == OMNI_BF16) verify_attn_combine_kernel<uint16_t><<<cgrid, 64, 0, s>>>(a);
-  else verify_attn_combine_kernel<float><<<cgrid, 64, 0, s>>>(a);
+  dim3 cgrid(tokens, heads, rows);
+  const int dpl = (head_dim + 63) / 64;  // output dimensions per lane
+#define OMNI_COMBINE(T_, DPL_) verify_attn_combine_kernel<T_, DPL_><<<cgrid, 64, 0, s>>>(a)
+  if (dtype == OMNI_BF16) {
+    if (dpl == 1) OMNI_COMBINE(uint16_t, 1);
+    else if (dpl == 2) OMNI_COMBINE(uint16_t, 2);
+    else if (dpl <= 4) OMNI_COMBINE(uint16_t, 4);
+    else OMNI_COMBINE(uint16_t, 8);
+  } else {
+    if (dpl == 1) OMNI_COMBINE(float, 1);
+    else if (dpl == 2) OMNI_COMBINE(float, 2);
+    else if (dpl <= 4) OMNI_COMBINE(float, 4);
+    else OMNI_COMBINE(float, 8);
+  }
+#undef OMNI_COMBINE
   return omni_launch_status();
 }

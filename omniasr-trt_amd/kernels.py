@@ -31,9 +31,10 @@ from . import _lib
 
 # Launch settings of draft_attention / decode_attention: ``chunk`` keys per split (0: the library's
 # choice for the launch shape), ``separate``: merge the splits in a second launch (else the last
-# split of each row and head merges them).
-DRAFT_ATTN = {"chunk": 0, "separate": False}
-ATTN = {"chunk": 0, "separate": False}
+# split of each row and head merges them after agent-scope fences -- an L2 write-back per wave on
+# gfx950, measured several times slower than the second launch).
+DRAFT_ATTN = {"chunk": 0, "separate": True}
+ATTN = {"chunk": 0, "separate": True}
 
 _counters: dict[int, torch.Tensor] = {}
 # Ticket buffers replaced by larger ones: captured graphs may still hold their addresses, so they

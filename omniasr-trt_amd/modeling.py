@@ -129,6 +129,7 @@ def random_decoder(cfg: DecoderConfig, *, std: float = 0.02, seed: int = 0, dtyp
                 p.fill_(1.0)
             else:
                 p.normal_(0.0, std, generator=g)
+    m.requires_grad_(False)
     m.rope = rope_table(cfg, device)
     return m.eval()
 

@@ -39,13 +39,14 @@ def test_workspace_and_split_queries():
     lib = _lib.load()
     for rows, t, h, d, keys in ((8, 5, 32, 128, 2560), (8, 1, 8, 512, 2048), (1, 9, 32, 128, 1280), (4, 3, 2, 16, 256)):
         chunk = lib.omni_verify_attention_chunk(rows, t, h, d, keys)
-        assert chunk % 64 == 0 and 64 <= chunk <= max(64, -(-keys // 32) * 32)
+        assert chunk % 32 == 0 and 32 <= chunk <= max(64, -(-keys // 32) * 32)
         splits = -(-keys // chunk)
         units = rows * h * splits * t
         want = -(-units * d * 4 // 256) * 256 + -(-units * 2 * 4 // 256) * 256
         assert lib.omni_verify_attention_workspace(rows, t, h, d, keys, 0) == want
-    # config 3: 8 rows x 32 heads, keys 2560 -> about 2048 waves over the chip
-    assert lib.omni_verify_attention_chunk(8, 5, 32, 128, 2560) == 320
+    # config 3: 8 rows x 32 heads, keys 2560 -> 320 keys for 2048 waves, capped at 8 tiles per split
+    assert lib.omni_verify_attention_chunk(8, 5, 32, 128, 2560) == 256
+    assert lib.omni_verify_attention_chunk(8, 5, 8, 512, 2048) == 64  # the real model's 8 heads
 
 
 FAKE = ctypes.c_void_p(0x10000)  # never dereferenced: every call below fails its checks before any launch
@@ -64,7 +65,7 @@ def test_argument_errors_before_launch():
     args[17] = 16
     assert lib.omni_verify_attention(*args) == -4
     args[17] = 1 << 30
-    args[13] = 100  # a split that is not a multiple of 64 keys
+    args[13] = 100  # a split that is not a multiple of 32 keys
     assert lib.omni_verify_attention(*args) == -1
     # rope: head_dim not a multiple of 8; nothing to do for zero tokens
     rope = [FAKE, 3 * 4 * 12, FAKE, 8192, FAKE, None, None, FAKE, FAKE, FAKE, 1, 1, 1, 8, 64, 5, 4, 12, _lib.BF16, None]

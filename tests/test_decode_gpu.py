@@ -93,7 +93,7 @@ def test_streams_across_calls(cuda):
 
 @pytest.mark.parametrize("draft_tokens", [1, 4, 8])
 def test_same_tokens_as_greedy(cuda, draft_tokens):
-    m, ref_dec = gpu_pair(21)
+    m, ref_dec = gpu_pair(24)  # seed 24: every context yields 7-44 greedy tokens
     ctxs = contexts(22, (40, 7, 251, 90, 13, 60))
     ref = [oref.greedy_reference(ref_dec, c) for c in ctxs]
     assert min(len(r) for r in ref) >= 3
@@ -146,7 +146,7 @@ def test_own_tokens_without_draft(cuda):
 
 
 def test_graph_replays_equal_eager_steps(cuda):
-    m, _ = gpu_pair(21)
+    m, _ = gpu_pair(24)
     ctxs = contexts(22, (40, 7, 251, 90, 13, 60))
     drafts = [(list(range(3, 12)) * 3, 0)] * len(ctxs)
     a = SpecDecoder(m, draft_tokens=4, max_batch=4, sync_every=3, reserve=8, graphs=True)
