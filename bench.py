@@ -104,6 +104,32 @@ class Workload:
                                                                     "start")}
         torch.cuda.synchronize()
 
+    def greedy_continuations(self, steps: int) -> list[list[int]]:
+        """Each slot's greedy tokens from the post-prefill state (the first fed token, then what the drafted loop
+        accepts in ``steps`` steps), the state restored afterwards."""
+        torch, dec, b = self.torch, self.dec, SLOTS
+        self.restore()
+        self.run(steps)
+        last = dec.last[:b].cpu().numpy()
+        out = dec.out[:b].cpu().numpy()
+        start = self.snapshot["last"].cpu().numpy()
+        conts = [[int(x) for x in out[s, start[s]: last[s] + 1]] for s in range(b)]
+        self.restore()
+        return conts
+
+    def set_drafts(self, drafts: list[list[int]] | None) -> None:
+        """Load a draft per slot as ``SpecDecoder.filled`` does (draft position 0 = the first generated token)."""
+        dec, b = self.dec, SLOTS
+        for s in range(b):
+            d = [] if drafts is None else drafts[s][: dec.draft.size(1)]
+            dec.draft[s] = -1
+            if d:
+                dec.draft[s, : len(d)] = self.torch.tensor(d, device="cuda", dtype=self.torch.int32)
+            dec.draft_len[s] = len(d)
+        dec.next[:b] = 1
+        self.snapshot["next"] = dec.next[:b].clone()
+        self.torch.cuda.synchronize()
+
     def restore(self):
         for k, v in self.snapshot.items():
             getattr(self.dec, k)[:SLOTS].copy_(v)
@@ -239,6 +265,83 @@ def time_small_kernels(pkg, torch, dec, reps: int = 200) -> dict:
             spec.AHEAD, spec.REACH, spec.SELF_WINDOW, spec.SELF_MIN)
     us = timed(lambda: kernels.spec_prepare(*args), reps)
     res["spec_prepare"] = {"us": round(us, 2)}
+    return res
+
+
+BEAMS = 5
+
+
+def beam_attention_bytes(ctx_len: np.ndarray, gen_len: int, rows: int, heads: int, dim: int) -> int:
+    """Algorithmic bytes of one beam-attention launch: each input's context K and V read once for all of its beams,
+    each row's generated K and V and pointers, q read and the output written (bf16)."""
+    ctx = int(np.sum(ctx_len)) * heads * dim * 2 * 2
+    gen = rows * gen_len * (heads * dim * 2 * 2 + 4)
+    return ctx + gen + 2 * rows * heads * dim * 2
+
+
+def beam_leg(pkg, torch, w: Workload, steps: int, warmup: int, reps: int) -> dict:
+    """Config 5 (beam variant): beam search with 5 beams and length norm over 8 inputs (40 rows) on the bench stack,
+    contexts of U[750, 2400] random embeddings.  ``steps`` replays of the step graph after ``warmup`` (host looks
+    and repetition checks aside), and the beam attention alone over the 12 layers' caches (HIP events)."""
+    beam, kernels = pkg.beam, pkg.kernels
+    dec = beam.BeamDecoder(w.model, beams=BEAMS, length_norm=True, max_batch=SLOTS, sync_every=16)
+    rng = np.random.default_rng(1006)
+    lengths = rng.integers(750, 2401, SLOTS)
+    g = torch.Generator(device="cuda").manual_seed(1006)
+    ctxs = [torch.randn(int(n), w.cfg.model_dim, device="cuda", generator=g).to(torch.bfloat16) for n in lengths]
+    dec.gdone[:] = True
+    dec.k_step[:] = 1
+    dec.tok.zero_()
+    beam._Groups(dec, SLOTS, iter(()), None, None).fill([(i, i, c) for i, c in enumerate(ctxs)])
+    dec.ensure_beam(dec.ccap, warmup + steps + 4)
+    ckeys = min(dec.ccap, beam.bucket(int(lengths.max())))
+    run = dec.beam_runner(SLOTS, ckeys)
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    live = int((~dec.gdone[:SLOTS]).sum())
+    # The attention alone: the step's shapes (40 rows, generated length 64), 24 launches cycling the 12 layers.
+    rows, heads, dim, gen = SLOTS * BEAMS, dec.heads, dec.head_dim, 64
+    q = torch.randn(rows, heads, dim, device="cuda", generator=g).to(torch.bfloat16)
+    ctx_len = torch.tensor(lengths, device="cuda")
+    gen_len = torch.full((rows,), gen, device="cuda", dtype=torch.long)
+    ptr = torch.randint(0, rows, (rows, dec.gcap), device="cuda", generator=g, dtype=torch.int32)
+    layers = len(dec.layers)
+    scale = dim ** -0.5
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        args = lambda i: (q, dec.kc[i], dec.vc[i], ctx_len, dec.kg[i], dec.vg[i], ptr, gen_len, BEAMS, ckeys, scale)
+        kernels.beam_attention(*args(0))
+        graph = torch.cuda.CUDAGraph()
+        graph.capture_begin()
+        for j in range(2 * layers):
+            kernels.beam_attention(*args(j % layers))
+        graph.capture_end()
+        graph.replay()
+        stream.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+        stream.synchronize()
+    torch.cuda.current_stream().wait_stream(stream)
+    us = e0.elapsed_time(e1) * 1000.0 / (reps * 2 * layers)
+    nbytes = beam_attention_bytes(lengths, gen, rows, heads, dim)
+    res = {"workload": "config 5b: 5 beams x 8 inputs, length norm, contexts U[750, 2400]", "steps": steps,
+           "ms_per_step": round(elapsed * 1e3 / steps, 4),
+           "best_beam_tokens_per_s": round(live * steps / elapsed, 2),
+           "row_tokens_per_s": round(live * BEAMS * steps / elapsed, 2),
+           "attention": {"us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1),
+                         "frac_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "generated_keys": gen,
+                         "ctx_keys": ckeys}}
+    dec.release()
     return res
 
 
@@ -380,6 +483,34 @@ def main() -> int:
         elapsed = time.perf_counter() - t0
     print(f"[bench] {args.steps} steps: {tokens} tokens in {elapsed * 1e3:.1f} ms", file=sys.stderr, flush=True)
 
+    ctc = None
+    if not args.no_extra:
+        # Config 5a: drafts from a synthetic CTC transcript = the greedy output with 10% random substitutions.
+        with torch.inference_mode():
+            conts = w.greedy_continuations(GENERATE + 16)  # the whole 300-token budget of every slot
+            rng = np.random.default_rng(1005)
+            drafts = [[int(rng.integers(3, w.cfg.vocab_size)) if rng.random() < 0.1 else t for t in c] for c in conts]
+            w.set_drafts(drafts)
+            w.run(args.warmup)
+            w.restore()
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            ctc_tokens, ctc_rows = w.run(args.steps)
+            torch.cuda.synchronize()
+            ctc_s = time.perf_counter() - t1
+            w.set_drafts(None)
+            w.restore()
+        ctc = {"workload": "config 5a: drafts = greedy output with 10% substitutions", "steps": args.steps,
+               "tokens": ctc_tokens, "tokens_per_s": round(ctc_tokens / ctc_s, 2),
+               "ms_per_step": round(ctc_s * 1e3 / args.steps, 4),
+               "tokens_per_row_step": round(ctc_tokens / max(ctc_rows, 1), 3)}
+        print(f"[bench] CTC drafts: {ctc_tokens} tokens in {ctc_s * 1e3:.1f} ms", file=sys.stderr, flush=True)
+    beams = None
+    if not args.no_extra:
+        with torch.inference_mode():
+            beams = beam_leg(pkg, torch, w, args.steps, args.warmup, args.attn_reps)
+        print(f"[bench] beam search: {beams['ms_per_step']} ms/step, attention {beams['attention']['us']} us",
+              file=sys.stderr, flush=True)
     with torch.inference_mode():
         attn = time_attention(pkg, torch, w.dec, DRAFT + 1, args.attn_reps)
         print(f"[bench] verify attention T=5: {attn['us']} us, {attn['GBps']} GB/s", file=sys.stderr, flush=True)
@@ -411,6 +542,8 @@ def main() -> int:
                      "achieved": attn["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": attn["frac_peak"],
                      "traffic": measured_traffic(), "bytes_per_launch": attn["bytes"], "us_per_launch": attn["us"]},
         "cpu_baseline": cpu,
+        "ctc_drafts": ctc,
+        "beam_search": beams,
         "attention_sweep": sweep,
         "kernels": extra,
     }

@@ -106,6 +106,36 @@ int omni_verify_attention(const void *q, const void *k_cache, const void *v_cach
                           void *out, void *workspace, size_t workspace_bytes, int32_t *counters,
                           int32_t flags, int32_t dtype, void *stream);
 
+/* Bytes of workspace omni_beam_attention needs for this shape and split size (0: default). */
+size_t omni_beam_attention_workspace(int32_t groups, int32_t beams, int32_t heads, int32_t head_dim,
+                                     int32_t ctx_keys, int32_t chunk);
+
+/*
+ * Beam-search attention.  Replaces ``kernels.beam_attention`` (``_beam_ctx`` with CAUSAL=False,
+ * ``_beam_gen``, ``_beam_combine``; src/omniasr_trt/kernels.py:309-332, 56-161) as called by
+ * ``BeamDecoder.attention`` (src/omniasr_trt/beam.py:107-112).
+ *
+ * ``q`` [groups*beams, heads, head_dim] contiguous: group g's beams are rows g*beams .. g*beams+beams-1.
+ * Row r = g*beams + i attends to the first ctx_len[g] keys of context row g (``k_ctx`` / ``v_ctx``,
+ * strides ctx_row / ctx_head / ctx_pos, ``ctx_cap`` positions, all within ``ctx_keys``), and to its
+ * generated keys j < gen_len[r], key j read at row ptr[r*ptr_stride + j] of ``k_gen`` / ``v_gen``
+ * (strides gen_row / gen_head / gen_pos, ``gen_rows`` rows of ``gen_cap`` positions); pointers are
+ * clamped into [0, gen_rows).  out = softmax(q.k * scale) . v over both parts, fp32 accumulation; no
+ * key at all gives zeros.  One pass over a group's context serves all of its beams (the MFMA kernel
+ * of omni_verify_attention with every query over the same keys); the generated keys are read by a
+ * pointer-chasing kernel into one more partial; a merge launch combines them.
+ * ``chunk``: context keys per split (0: the library's choice).  ``workspace``: at least
+ * omni_beam_attention_workspace() bytes, 256-byte aligned.  beams: 1..16.
+ */
+int omni_beam_attention(const void *q, const void *k_ctx, const void *v_ctx, int64_t ctx_row,
+                        int64_t ctx_head, int64_t ctx_pos, int64_t ctx_cap, const int64_t *ctx_len,
+                        const void *k_gen, const void *v_gen, int64_t gen_row, int64_t gen_head,
+                        int64_t gen_pos, int64_t gen_cap, int64_t gen_rows, const int32_t *ptr,
+                        int64_t ptr_stride, const int64_t *gen_len, int32_t groups, int32_t beams,
+                        int32_t heads, int32_t head_dim, int32_t ctx_keys, int32_t chunk, float scale,
+                        void *out, void *workspace, size_t workspace_bytes, int32_t dtype,
+                        void *stream);
+
 /*
  * Draft proposal of every row.  Replaces ``kernels.propose`` / ``_propose``
  * (src/omniasr_trt/kernels.py:361-377, 214-268) as called by ``SpecDecoder.propose``

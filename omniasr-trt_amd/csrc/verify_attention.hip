@@ -46,6 +46,9 @@ struct AttnArgs {
   int* counters;     // [rows * H]
   void* out;         // [rows * T, H, D]
   int separate;      // partials only: a second launch merges them
+  int causal;        // 1: query i sees lengths + i keys (drafted step); 0: every query sees lengths keys (beams)
+  int ctx_splits;    // key splits of the grid (= splits, or splits - 1 with a generated-keys split)
+  int gen_split;     // partial slot of the beams' generated keys (merged with the key splits), or -1
 };
 
 struct SplitRange {
@@ -59,9 +62,9 @@ struct SplitRange {
 __device__ __forceinline__ SplitRange split_range(const AttnArgs& a, int b, int sp) {
   SplitRange r;
   r.n = clamp64(a.lengths[b], 0, a.cache_len);
-  int64_t total = r.n + a.T - 1;  // keys the last query sees
+  int64_t total = r.n + (a.causal ? a.T - 1 : 0);  // keys the last query sees
   total = total < a.cache_len ? total : a.cache_len;
-  const int64_t covered = (int64_t)a.splits * a.chunk;
+  const int64_t covered = (int64_t)a.ctx_splits * a.chunk;
   total = total < covered ? total : covered;
   r.total = total;
   int64_t nact = ceil_div64(total, a.chunk);
@@ -88,31 +91,40 @@ __device__ __forceinline__ void store4<uint16_t>(uint16_t* p, f32x4_t v) {
   *reinterpret_cast<uint2*>(p) = w;
 }
 
-// Log-sum-exp merge of the ``nact`` partials of (row b, head h) by one wave; writes the output.
+// Partial slot of the q-th partial to merge: the row's key splits, then the generated-keys slot if any.
+__device__ __forceinline__ int merge_slot(const AttnArgs& a, int nact, int q) {
+  return q < nact ? q : a.gen_split;
+}
+
+// Log-sum-exp merge of the partials of (row b, head h) by one wave; writes the output.
 template <typename OutT>
 __device__ void merge_splits(const AttnArgs& a, int b, int h, int nact) {
   const int lane = lane_id();
+  const int nq = nact + (a.gen_split >= 0 ? 1 : 0);
   const int64_t split0 = ((int64_t)b * a.H + h) * a.splits;
   OutT* out = reinterpret_cast<OutT*>(a.out);
   for (int t = 0; t < a.T; ++t) {
     float top = -INFINITY;
-    for (int s = lane; s < nact; s += kWave) top = fmaxf(top, a.part_ml[((split0 + s) * a.T + t) * 2]);
+    for (int q = lane; q < nq; q += kWave)
+      top = fmaxf(top, a.part_ml[((split0 + merge_slot(a, nact, q)) * a.T + t) * 2]);
     top = wave_max(top);
     float den = 0.f;
-    for (int s = lane; s < nact; s += kWave) {
-      const float m = a.part_ml[((split0 + s) * a.T + t) * 2];
+    for (int q = lane; q < nq; q += kWave) {
+      const int64_t ml = ((split0 + merge_slot(a, nact, q)) * a.T + t) * 2;
+      const float m = a.part_ml[ml];
       const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - top);
-      den += w * a.part_ml[((split0 + s) * a.T + t) * 2 + 1];
+      den += w * a.part_ml[ml + 1];
     }
     den = wave_sum(den);
     const float div = den > 0.f ? den : 1.f;
     OutT* orow = out + ((int64_t)(b * a.T + t) * a.H + h) * a.D;
     for (int d = lane * 4; d < a.D; d += kWave * 4) {
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-      for (int s = 0; s < nact; ++s) {
-        const float m = a.part_ml[((split0 + s) * a.T + t) * 2];
+      for (int q = 0; q < nq; ++q) {
+        const int64_t slot = (split0 + merge_slot(a, nact, q)) * a.T + t;
+        const float m = a.part_ml[slot * 2];
         const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - top);
-        const f32x4_t po = *reinterpret_cast<const f32x4_t*>(a.part_o + ((split0 + s) * a.T + t) * a.D + d);
+        const f32x4_t po = *reinterpret_cast<const f32x4_t*>(a.part_o + slot * a.D + d);
         acc += w * po;
       }
       store4<OutT>(orow + d, acc / div);
@@ -395,7 +407,8 @@ __global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(Attn
       vt += tile_bytes;
     }
   }
-  const int64_t lim_c = (r.n + c) < r.total ? (r.n + c) : r.total;  // query c's key limit
+  const int64_t own = r.n + (a.causal ? c : 0);
+  const int64_t lim_c = own < r.total ? own : r.total;  // query c's key limit
   for (int64_t ti = sp + nfull * r.nact; ti < row_tiles; ti += r.nact) {  // the row's last one or two tiles
     const int64_t kb = ti * 32;
     load_tail_tile<D>(A, kbase, vbase, kb, r.total, last_key, a.s_pos, c, g);
@@ -408,7 +421,7 @@ __global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(Attn
   float li[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) li[i] = __shfl(l_tot, 4 * g + i, kWave);
-  if (r.nact == 1) {
+  if (r.nact == 1 && a.gen_split < 0) {
     uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -500,7 +513,8 @@ __global__ __launch_bounds__(64) void verify_attn_valu_kernel(AttnArgs a) {
 #pragma unroll
     for (int t = 0; t < kValuMaxT; ++t) {
       if (t >= T) continue;  // T is uniform: the whole wave skips together
-      const int64_t lim = (r.n + t) < r.stop ? (r.n + t) : r.stop;
+      const int64_t own = r.n + (a.causal ? t : 0);
+      const int64_t lim = own < r.stop ? own : r.stop;
       const float sc = key < lim ? s[t] : -INFINITY;
       const float m_new = fmaxf(m_run[t], wave_max(sc));
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
@@ -530,7 +544,7 @@ __global__ __launch_bounds__(64) void verify_attn_valu_kernel(AttnArgs a) {
     __syncthreads();
   }
 
-  const bool direct = r.nact == 1;
+  const bool direct = r.nact == 1 && a.gen_split < 0;
   const int64_t base = (((int64_t)b * a.H + h) * a.splits + sp) * T;
   Elem* out = reinterpret_cast<Elem*>(a.out);
 #pragma unroll
@@ -572,12 +586,13 @@ __global__ __launch_bounds__(64) void verify_attn_combine_kernel(AttnArgs a) {
   const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const SplitRange r = split_range(a, b, 0);
   const int nact = r.nact;
-  if (nact == 1) return;  // written directly by its only split
+  if (nact == 1 && a.gen_split < 0) return;  // written directly by its only split
+  const int nq = nact + (a.gen_split >= 0 ? 1 : 0);  // partials to merge
   const int lane = threadIdx.x;
   const int T = a.T, D = a.D;
   const int64_t split0 = ((int64_t)b * a.H + h) * a.splits;
   OutT* orow = reinterpret_cast<OutT*>(a.out) + ((int64_t)(b * T + t) * a.H + h) * D;
-  if (nact > kCombineMaxSplits) {  // beyond the unrolled case: the generic merge
+  if (nq > kCombineMaxSplits) {  // beyond the unrolled case: the generic merge
     if (t == 0) merge_splits<OutT>(a, b, h, nact);
     return;
   }
@@ -586,16 +601,17 @@ __global__ __launch_bounds__(64) void verify_attn_combine_kernel(AttnArgs a) {
   float po[kCombineMaxSplits][DPL];
 #pragma unroll
   for (int s = 0; s < kCombineMaxSplits; ++s) {
-    if (s < nact && has_d) {
-      const float* src = a.part_o + ((split0 + s) * T + t) * D + d0;
+    if (s < nq && has_d) {
+      const float* src = a.part_o + ((split0 + merge_slot(a, nact, s)) * T + t) * D + d0;
 #pragma unroll
       for (int e = 0; e < DPL; ++e) po[s][e] = src[e];
     }
   }
   float m = -INFINITY, l = 0.f;
-  if (lane < nact) {
-    m = a.part_ml[((split0 + lane) * T + t) * 2];
-    l = a.part_ml[((split0 + lane) * T + t) * 2 + 1];
+  if (lane < nq) {
+    const int64_t ml = ((split0 + merge_slot(a, nact, lane)) * T + t) * 2;
+    m = a.part_ml[ml];
+    l = a.part_ml[ml + 1];
   }
   const float top = wave_max(m);
   const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - top);
@@ -606,7 +622,7 @@ __global__ __launch_bounds__(64) void verify_attn_combine_kernel(AttnArgs a) {
   for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
 #pragma unroll
   for (int s = 0; s < kCombineMaxSplits; ++s) {
-    if (s < nact) {
+    if (s < nq) {
       const float ws = __shfl(w, s, kWave);
 #pragma unroll
       for (int e = 0; e < DPL; ++e) acc[e] += ws * po[s][e];
@@ -656,6 +672,64 @@ extern "C" size_t omni_verify_attention_workspace(int32_t rows, int32_t tokens, 
   return align256(units * head_dim * sizeof(float)) + align256(units * 2 * sizeof(float));
 }
 
+// Key-split kernel and (when asked) the merge launch for filled-in arguments.
+static int launch_attention(const AttnArgs& a, int rows, int dtype, hipStream_t s) {
+  const bool mfma = dtype == OMNI_BF16 && a.D % 128 == 0;
+  dim3 grid(a.ctx_splits, a.H, rows);
+  if (mfma) {
+    switch (a.D) {
+      case 128: verify_attn_mfma_kernel<128, true><<<grid, 64, 0, s>>>(a); break;
+      case 256: verify_attn_mfma_kernel<256, false><<<grid, 64, 0, s>>>(a); break;
+      case 512: verify_attn_mfma_kernel<512, false><<<grid, 64, 0, s>>>(a); break;
+      default: verify_attn_valu_kernel<uint16_t><<<grid, 64, 0, s>>>(a); break;
+    }
+  } else if (dtype == OMNI_BF16) {
+    verify_attn_valu_kernel<uint16_t><<<grid, 64, 0, s>>>(a);
+  } else {
+    verify_attn_valu_kernel<float><<<grid, 64, 0, s>>>(a);
+  }
+  return omni_launch_status();
+}
+
+static int launch_combine(const AttnArgs& a, int rows, int dtype, hipStream_t s) {
+  dim3 cgrid(a.T, a.H, rows);
+  const int dpl = (a.D + 63) / 64;  // output dimensions per lane
+#define OMNI_COMBINE(T_, DPL_) verify_attn_combine_kernel<T_, DPL_><<<cgrid, 64, 0, s>>>(a)
+  if (dtype == OMNI_BF16) {
+    if (dpl == 1) OMNI_COMBINE(uint16_t, 1);
+    else if (dpl == 2) OMNI_COMBINE(uint16_t, 2);
+    else if (dpl <= 4) OMNI_COMBINE(uint16_t, 4);
+    else OMNI_COMBINE(uint16_t, 8);
+  } else {
+    if (dpl == 1) OMNI_COMBINE(float, 1);
+    else if (dpl == 2) OMNI_COMBINE(float, 2);
+    else if (dpl <= 4) OMNI_COMBINE(float, 4);
+    else OMNI_COMBINE(float, 8);
+  }
+#undef OMNI_COMBINE
+  return omni_launch_status();
+}
+
+static int check_attention_shape(int32_t tokens, int32_t heads, int32_t head_dim, int32_t dtype, float scale) {
+  if (heads <= 0 || head_dim <= 0) return OMNI_ERR_INVALID;
+  if (!(scale > 0.f)) return OMNI_ERR_INVALID;  // a softmax scale is positive (head_dim^-1/2)
+  if (tokens < 1 || tokens > 16) return OMNI_ERR_SHAPE;
+  if (dtype != OMNI_BF16 && dtype != OMNI_F32) return OMNI_ERR_DTYPE;
+  if (head_dim % 8 != 0 || head_dim > kValuMaxD) return OMNI_ERR_SHAPE;
+  return OMNI_OK;
+}
+
+// 128-bit operand loads: q and out, and on the MFMA path every row / head / position start, 16-byte aligned.
+static bool attention_aligned(const void* q, const void* out, const void* k, const void* v, int64_t s_row,
+                              int64_t s_head, int64_t s_pos, int32_t head_dim, int32_t dtype) {
+  if (((uintptr_t)q | (uintptr_t)out) & 15u) return false;
+  if (dtype == OMNI_BF16 && head_dim % 128 == 0) {
+    if (((uintptr_t)k | (uintptr_t)v) & 15u) return false;
+    if ((s_row | s_head | s_pos) % 8 != 0) return false;
+  }
+  return true;
+}
+
 extern "C" int omni_verify_attention(const void* q, const void* k_cache, const void* v_cache,
                                      int64_t stride_row, int64_t stride_head, int64_t stride_pos,
                                      int64_t cache_len, const int64_t* lengths, int32_t rows,
@@ -663,25 +737,18 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
                                      int32_t chunk, float scale, void* out, void* workspace,
                                      size_t workspace_bytes, int32_t* counters, int32_t flags,
                                      int32_t dtype, void* stream) {
-  if (rows < 0 || heads <= 0 || head_dim <= 0 || keys <= 0 || cache_len <= 0) return OMNI_ERR_INVALID;
-  if (!(scale > 0.f)) return OMNI_ERR_INVALID;  // a softmax scale is positive (head_dim^-1/2)
+  if (rows < 0 || keys <= 0 || cache_len <= 0) return OMNI_ERR_INVALID;
+  int st = check_attention_shape(tokens, heads, head_dim, dtype, scale);
+  if (st != OMNI_OK) return st;
   if (rows == 0) return OMNI_OK;
   if (!q || !k_cache || !v_cache || !lengths || !out || !workspace || !counters) return OMNI_ERR_INVALID;
-  if (tokens < 1 || tokens > 16) return OMNI_ERR_SHAPE;
-  if (dtype != OMNI_BF16 && dtype != OMNI_F32) return OMNI_ERR_DTYPE;
-  if (head_dim % 8 != 0 || head_dim > kValuMaxD) return OMNI_ERR_SHAPE;
   if (chunk == 0) chunk = omni_verify_attention_chunk(rows, tokens, heads, head_dim, keys);
   if (chunk <= 0 || chunk % 32 != 0) return OMNI_ERR_INVALID;
   if (workspace_bytes < omni_verify_attention_workspace(rows, tokens, heads, head_dim, keys, chunk))
     return OMNI_ERR_WORKSPACE;
   if (((uintptr_t)workspace & 255u) != 0) return OMNI_ERR_WORKSPACE;
-  const bool mfma = dtype == OMNI_BF16 && head_dim % 128 == 0;
-  // Vector accesses: q, out (and, on MFMA, every row / head / position start) 16-byte aligned.
-  if (((uintptr_t)q | (uintptr_t)out) & 15u) return OMNI_ERR_INVALID;
-  if (mfma) {
-    if (((uintptr_t)k_cache | (uintptr_t)v_cache) & 15u) return OMNI_ERR_INVALID;
-    if ((stride_row | stride_head | stride_pos) % 8 != 0) return OMNI_ERR_INVALID;
-  }
+  if (!attention_aligned(q, out, k_cache, v_cache, stride_row, stride_head, stride_pos, head_dim, dtype))
+    return OMNI_ERR_INVALID;
   const int splits = attn_splits(keys, chunk);
   const size_t units = (size_t)rows * heads * splits * tokens;
   AttnArgs a;
@@ -704,36 +771,225 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
   a.counters = counters;
   a.out = out;
   a.separate = (flags & OMNI_ATTN_SEPARATE_COMBINE) ? 1 : 0;
+  a.causal = 1;
+  a.ctx_splits = splits;
+  a.gen_split = -1;
   hipStream_t s = (hipStream_t)stream;
-  dim3 grid(splits, heads, rows);
-  if (mfma) {
-    switch (head_dim) {
-      case 128: verify_attn_mfma_kernel<128, true><<<grid, 64, 0, s>>>(a); break;
-      case 256: verify_attn_mfma_kernel<256, false><<<grid, 64, 0, s>>>(a); break;
-      case 512: verify_attn_mfma_kernel<512, false><<<grid, 64, 0, s>>>(a); break;
-      default: verify_attn_valu_kernel<uint16_t><<<grid, 64, 0, s>>>(a); break;
-    }
-  } else if (dtype == OMNI_BF16) {
-    verify_attn_valu_kernel<uint16_t><<<grid, 64, 0, s>>>(a);
-  } else {
-    verify_attn_valu_kernel<float><<<grid, 64, 0, s>>>(a);
-  }
-  int st = omni_launch_status();
+  st = launch_attention(a, rows, dtype, s);
   if (st != OMNI_OK || !a.separate) return st;
-  dim3 cgrid(tokens, heads, rows);
-  const int dpl = (head_dim + 63) / 64;  // output dimensions per lane
-#define OMNI_COMBINE(T_, DPL_) verify_attn_combine_kernel<T_, DPL_><<<cgrid, 64, 0, s>>>(a)
-  if (dtype == OMNI_BF16) {
-    if (dpl == 1) OMNI_COMBINE(uint16_t, 1);
-    else if (dpl == 2) OMNI_COMBINE(uint16_t, 2);
-    else if (dpl <= 4) OMNI_COMBINE(uint16_t, 4);
-    else OMNI_COMBINE(uint16_t, 8);
-  } else {
-    if (dpl == 1) OMNI_COMBINE(float, 1);
-    else if (dpl == 2) OMNI_COMBINE(float, 2);
-    else if (dpl <= 4) OMNI_COMBINE(float, 4);
-    else OMNI_COMBINE(float, 8);
+  return launch_combine(a, rows, dtype, s);
+}
+
+// ---------------------------------------------------------------------------------------------- beams
+
+namespace omni {
+
+struct BeamGenArgs {
+  const void* q;  // [groups * beams, H, D]
+  const void* kg;
+  const void* vg;
+  int64_t s_row, s_head, s_pos, gen_cap, gen_rows;
+  const int32_t* ptr;  // [groups * beams, ptr_stride]: row that wrote position j of row r's history
+  int64_t ptr_stride;
+  const int64_t* gen_len;  // [groups * beams]
+  int beams, H, D;
+  float scale_log2;
+  float* part_o;
+  float* part_ml;
+  int splits, gen_split;
+};
+
+template <typename Elem>
+__device__ __forceinline__ void load8(const Elem* p, float (&x)[8]);
+
+template <>
+__device__ __forceinline__ void load8<uint16_t>(const uint16_t* p, float (&x)[8]) {
+  const u32x4_t v = *reinterpret_cast<const u32x4_t*>(p);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = bf16x8_elem(v, e);
+}
+
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float (&x)[8]) {
+  const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(p);
+  const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[e] = lo[e];
+    x[e + 4] = hi[e];
   }
-#undef OMNI_COMBINE
-  return omni_launch_status();
+}
+
+// Row r's generated keys j < gen_len[r], each read from the row that wrote it (ptr[r, j]): one wave per
+// (head, row), 64 keys per pass.  Scores: one key per lane, 16-byte loads along its row.  P V: D/8 lanes per
+// key (8 dimensions each, 16-byte loads), 64/(D/8) keys at once, summed over the key groups at the end.  The
+// result is a partial in the generated-keys slot, merged with the context splits by the merge launch.
+// (``_beam_gen``, src/omniasr_trt/kernels.py:115-144.)
+template <typename Elem>
+__global__ __launch_bounds__(64) void beam_gen_kernel(BeamGenArgs a) {
+  __shared__ float qs[kValuMaxD];
+  __shared__ float ps[kWave];
+  __shared__ int64_t off_sh[kWave];
+  __shared__ float red[kWave * 8];  // kpar * D <= 64 * 8
+  const int h = blockIdx.x, r = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int D = a.D;
+  const int64_t n = clamp64(a.gen_len[r], 0, a.gen_cap);
+  const Elem* qrow = reinterpret_cast<const Elem*>(a.q) + ((int64_t)r * a.H + h) * D;
+  for (int d = lane; d < D; d += kWave) qs[d] = load_elem<Elem>(qrow + d) * a.scale_log2;
+  __syncthreads();
+  const Elem* kb = reinterpret_cast<const Elem*>(a.kg) + h * a.s_head;
+  const Elem* vb = reinterpret_cast<const Elem*>(a.vg) + h * a.s_head;
+  const int lpk = D / 8;  // lanes per key in P V
+  const int kpar = kWave / lpk;
+  const int grp = lane / lpk, sub = lane - grp * lpk;
+  const bool pv_lane = grp < kpar;
+  float m_run = -INFINITY, l_run = 0.f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int64_t j0 = 0; j0 < n; j0 += kWave) {
+    const int64_t j = j0 + lane;
+    const bool valid = j < n;
+    int64_t src = valid ? (int64_t)a.ptr[(int64_t)r * a.ptr_stride + j] : 0;
+    src = clamp64(src, 0, a.gen_rows - 1);
+    const int64_t off = src * a.s_row + (valid ? j : 0) * a.s_pos;
+    float sc = 0.f;
+    for (int d0 = 0; d0 < D; d0 += 8) {
+      float x[8];
+      load8<Elem>(kb + off + d0, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sc = fmaf(qs[d0 + e], x[e], sc);
+    }
+    sc = valid ? sc : -INFINITY;
+    const float m_new = fmaxf(m_run, wave_max(sc));
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // m_new is finite: key j0 is valid
+    const float pr = __builtin_amdgcn_exp2f(sc - m_new);
+    l_run = l_run * alpha + pr;
+    m_run = m_new;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+    ps[lane] = pr;
+    off_sh[lane] = off;
+    __syncthreads();
+    const int kend = (int)((n - j0) < kWave ? (n - j0) : kWave);
+    if (pv_lane) {
+      for (int kk = grp; kk < kend; kk += kpar) {
+        float x[8];
+        load8<Elem>(vb + off_sh[kk] + sub * 8, x);
+        const float p = ps[kk];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = fmaf(p, x[e], acc[e]);
+      }
+    }
+    __syncthreads();
+  }
+  const float l_tot = wave_sum(l_run);
+  if (pv_lane) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[grp * D + sub * 8 + e] = acc[e];
+  }
+  __syncthreads();
+  const int g = r / a.beams, i = r - g * a.beams;
+  const int64_t slot = (((int64_t)g * a.H + h) * a.splits + a.gen_split) * a.beams + i;
+  for (int d = lane; d < D; d += kWave) {
+    float o = 0.f;
+    for (int q = 0; q < kpar; ++q) o += red[q * D + d];
+    a.part_o[slot * D + d] = o;
+  }
+  if (lane == 0) {
+    a.part_ml[slot * 2] = m_run;
+    a.part_ml[slot * 2 + 1] = l_tot;
+  }
+}
+
+}  // namespace omni
+
+extern "C" size_t omni_beam_attention_workspace(int32_t groups, int32_t beams, int32_t heads, int32_t head_dim,
+                                                int32_t ctx_keys, int32_t chunk) {
+  if (groups <= 0 || beams <= 0 || heads <= 0 || head_dim <= 0 || ctx_keys <= 0) return 0;
+  if (chunk <= 0) chunk = omni_verify_attention_chunk(groups, beams, heads, head_dim, ctx_keys);
+  const size_t splits = (size_t)attn_splits(ctx_keys, chunk) + 1;
+  const size_t units = (size_t)groups * heads * splits * beams;
+  return align256(units * head_dim * sizeof(float)) + align256(units * 2 * sizeof(float));
+}
+
+extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void* v_ctx, int64_t ctx_row,
+                                   int64_t ctx_head, int64_t ctx_pos, int64_t ctx_cap, const int64_t* ctx_len,
+                                   const void* k_gen, const void* v_gen, int64_t gen_row, int64_t gen_head,
+                                   int64_t gen_pos, int64_t gen_cap, int64_t gen_rows, const int32_t* ptr,
+                                   int64_t ptr_stride, const int64_t* gen_len, int32_t groups, int32_t beams,
+                                   int32_t heads, int32_t head_dim, int32_t ctx_keys, int32_t chunk, float scale,
+                                   void* out, void* workspace, size_t workspace_bytes, int32_t dtype,
+                                   void* stream) {
+  if (groups < 0 || ctx_keys <= 0 || ctx_cap <= 0 || gen_cap <= 0 || gen_rows <= 0) return OMNI_ERR_INVALID;
+  int st = check_attention_shape(beams, heads, head_dim, dtype, scale);
+  if (st != OMNI_OK) return st;
+  if (groups == 0) return OMNI_OK;
+  if (!q || !k_ctx || !v_ctx || !ctx_len || !k_gen || !v_gen || !ptr || !gen_len || !out || !workspace)
+    return OMNI_ERR_INVALID;
+  if (ptr_stride < gen_cap) return OMNI_ERR_INVALID;
+  // The generated-keys kernel reads 8 elements (16 or 32 bytes) at a time along every row.
+  if ((((uintptr_t)k_gen | (uintptr_t)v_gen) & 15u) || (gen_row | gen_head | gen_pos) % 8 != 0)
+    return OMNI_ERR_INVALID;
+  if (chunk == 0) chunk = omni_verify_attention_chunk(groups, beams, heads, head_dim, ctx_keys);
+  if (chunk <= 0 || chunk % 32 != 0) return OMNI_ERR_INVALID;
+  if (workspace_bytes < omni_beam_attention_workspace(groups, beams, heads, head_dim, ctx_keys, chunk))
+    return OMNI_ERR_WORKSPACE;
+  if (((uintptr_t)workspace & 255u) != 0) return OMNI_ERR_WORKSPACE;
+  if (!attention_aligned(q, out, k_ctx, v_ctx, ctx_row, ctx_head, ctx_pos, head_dim, dtype)) return OMNI_ERR_INVALID;
+  const int ctx_splits = attn_splits(ctx_keys, chunk);
+  const int splits = ctx_splits + 1;
+  const size_t units = (size_t)groups * heads * splits * beams;
+  AttnArgs a;
+  a.q = q;
+  a.k = k_ctx;
+  a.v = v_ctx;
+  a.s_row = ctx_row;
+  a.s_head = ctx_head;
+  a.s_pos = ctx_pos;
+  a.cache_len = ctx_cap;
+  a.lengths = ctx_len;
+  a.T = beams;  // a group's beams are its queries, all over the same context keys
+  a.H = heads;
+  a.D = head_dim;
+  a.chunk = chunk;
+  a.splits = splits;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.part_o = (float*)workspace;
+  a.part_ml = (float*)((char*)workspace + align256(units * head_dim * sizeof(float)));
+  a.counters = nullptr;
+  a.out = out;
+  a.separate = 1;
+  a.causal = 0;
+  a.ctx_splits = ctx_splits;
+  a.gen_split = ctx_splits;
+  hipStream_t s = (hipStream_t)stream;
+  st = launch_attention(a, groups, dtype, s);
+  if (st != OMNI_OK) return st;
+  BeamGenArgs gargs;
+  gargs.q = q;
+  gargs.kg = k_gen;
+  gargs.vg = v_gen;
+  gargs.s_row = gen_row;
+  gargs.s_head = gen_head;
+  gargs.s_pos = gen_pos;
+  gargs.gen_cap = gen_cap;
+  gargs.gen_rows = gen_rows;
+  gargs.ptr = ptr;
+  gargs.ptr_stride = ptr_stride;
+  gargs.gen_len = gen_len;
+  gargs.beams = beams;
+  gargs.H = heads;
+  gargs.D = head_dim;
+  gargs.scale_log2 = a.scale_log2;
+  gargs.part_o = a.part_o;
+  gargs.part_ml = a.part_ml;
+  gargs.splits = splits;
+  gargs.gen_split = ctx_splits;
+  dim3 ggrid(heads, groups * beams);
+  if (dtype == OMNI_BF16) beam_gen_kernel<uint16_t><<<ggrid, 64, 0, s>>>(gargs);
+  else beam_gen_kernel<float><<<ggrid, 64, 0, s>>>(gargs);
+  st = omni_launch_status();
+  if (st != OMNI_OK) return st;
+  return launch_combine(a, groups, dtype, s);
 }

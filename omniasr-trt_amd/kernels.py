@@ -173,6 +173,43 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
                    ATTN["separate"])
 
 
+def beam_attention(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, ctx_len: torch.Tensor, kg: torch.Tensor,
+                   vg: torch.Tensor, ptr: torch.Tensor, gen_len: torch.Tensor, beams: int, ctx_keys: int,
+                   scale: float, chunk: int = 0) -> torch.Tensor:
+    """Beam rows ``q`` [S*N, H, D] (input g's beams are rows g*N .. g*N+N-1): attention over input g's context
+    ``kc``/``vc`` [>=S, H, C, D] (first ``ctx_len[g]`` keys, all within ``ctx_keys``) and row r's generated keys
+    ``kg``/``vg`` [>=S*N, H, G, D], position j read from row ``ptr[r, j]`` (first ``gen_len[r]``).  One pass over
+    a group's context serves all of its beams.  Returns [S*N, H, D] in q's dtype.
+    (src/omniasr_trt/kernels.py:309-332)"""
+    lib = _lib.load()
+    rows, heads, dim = q.shape
+    _need(beams >= 1 and rows % beams == 0, "q: [S*N, H, D]")
+    groups = rows // beams
+    _need(q.is_contiguous(), "q: contiguous [S*N, H, D]")
+    for name, a, b in (("kc / vc", kc, vc), ("kg / vg", kg, vg)):
+        _need(a.dtype == q.dtype == b.dtype, f"q and {name}: one dtype")
+        _need(a.stride() == b.stride() and a.shape == b.shape, f"{name}: same layout")
+        _need(a.dim() == 4 and a.stride(3) == 1 and a.size(3) == dim and a.size(1) == heads,
+              f"{name}: [rows, H, positions, D] with unit stride in D")
+    _need(kc.size(0) >= groups, "kc: at least S rows")
+    _need(kg.size(0) >= rows, "kg: at least S*N rows")
+    _need(ptr.dtype == torch.int32 and ptr.dim() == 2 and ptr.stride(1) == 1 and ptr.size(0) >= rows
+          and ptr.size(1) >= kg.size(2), "ptr: [>=S*N, >=G] int32 with unit stride in positions")
+    _index(ctx_len, "ctx_len")
+    _index(gen_len, "gen_len")
+    _need(ctx_len.numel() >= groups and gen_len.numel() >= rows, "ctx_len: [S], gen_len: [S*N]")
+    ws = lib.omni_beam_attention_workspace(groups, beams, heads, dim, ctx_keys, int(chunk))
+    workspace = torch.empty(max(ws, 256), device=q.device, dtype=torch.uint8)
+    out = torch.empty_like(q)
+    status = lib.omni_beam_attention(
+        q.data_ptr(), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.size(2),
+        ctx_len.data_ptr(), kg.data_ptr(), vg.data_ptr(), kg.stride(0), kg.stride(1), kg.stride(2), kg.size(2),
+        kg.size(0), ptr.data_ptr(), ptr.stride(0), gen_len.data_ptr(), groups, beams, heads, dim, int(ctx_keys),
+        int(chunk), float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel(), _dtype(q), _stream(q))
+    _lib.check(status, "beam attention")
+    return out
+
+
 def splits_for(rows: int, heads: int, keys: int, block: int = 64, programs: int = 264) -> tuple[int, int]:
     """Key splits (a power of two, about ``programs`` programs in all) and the keys each split covers -- the
     reference's rule for its Triton launches (src/omniasr_trt/kernels.py:393-400), kept for callers that use it;

@@ -1,6 +1,7 @@
 """Reference-order greedy decoding on the CPU in float64 (test infrastructure; see oracle/__init__.py).
 
-Restates ``LLMTranscriber.greedy_reference`` (src/omniasr_trt/llm.py:182-203) over ``decoder_forward``
+Restates ``LLMTranscriber.greedy_reference`` and ``beam_reference`` (src/omniasr_trt/llm.py:182-254) over
+``decoder_forward``
 (src/omniasr_trt/modeling.py:374-406): prefill all of a context but its final <bos>, then one token at a time,
 greedy on the log-softmax, stopping at EOS, at position ``limit``, or at the zlib repetition stop.  Attention is
 written out (masked softmax) instead of calling SDPA.  The decoder's weights are read from a model with the
@@ -115,3 +116,59 @@ def greedy_reference(dec: Fp64Decoder, ctx: torch.Tensor, limit: int = MAX_GEN -
         x = dec.embed(token)
         t += 1
     return [int(v) for v in out[c - 1: t + 1] if v not in (PAD, BOS, EOS)]
+
+
+@torch.inference_mode()
+def beam_reference(dec: Fp64Decoder, ctx: torch.Tensor, beams: int, length_norm: bool = False,
+                   limit: int = MAX_GEN - 4) -> list[int]:
+    """Beam search of one context [C, D] in the reference's order of computation (src/omniasr_trt/llm.py:205-254).
+
+    ``beams`` hypotheses, each with its own K/V cache; at the first step only hypothesis 0 is live (the others
+    score -1e6).  Every step a hypothesis offers score + log p for every token (``length_norm``: (score * c +
+    log p) / (c + 1) with c its count of tokens other than PAD / EOS, used once hypothesis 0's count is above 0),
+    a finished one only EOS at its frozen score; the best ``beams`` offers survive (sorted, ties to the lower
+    flat index) and take their parents' caches, histories, scores and states.  The repetition stop ends the
+    hypotheses whose last 100 tokens compress more than 4x at the checked positions.  The text is hypothesis 0's.
+    Pinned by: one beam is ``greedy_reference``; with as many beams as tokens and a stop after two tokens, the
+    result is the best of all two-token sequences by brute force (tests/test_oracle.py).
+    """
+    ctx = ctx.detach().to("cpu", torch.float64)
+    c, n = ctx.size(0), beams
+    caches = [[None] * dec.layers for _ in range(n)]
+    if c > 1:
+        dec.forward(ctx[: c - 1], torch.arange(c - 1), caches[0])
+        for b in range(1, n):
+            caches[b] = [(k.clone(), v.clone()) for k, v in caches[0]]
+    out = np.full((n, MAX_GEN), PAD, dtype=np.int64)
+    scores = np.full(n, -1e6)
+    scores[0] = 0.0
+    ended = np.zeros(n, dtype=bool)
+    xs = [ctx[c - 1]] * n
+    t = c - 1
+    while True:
+        logp = np.stack([F.log_softmax(dec.logits(dec.forward(xs[b][None], torch.tensor([t]), caches[b])[0]), -1)
+                         .numpy() for b in range(n)])  # [n, V]
+        count = ((out[:, :t] != PAD) & (out[:, :t] != EOS)).sum(1)[:, None]
+        if length_norm and count[0, 0] > 0:
+            cand = (scores[:, None] * count + logp) / (count + 1)
+        else:
+            cand = scores[:, None] + logp
+        cand[ended] = -np.inf
+        cand[ended, EOS] = scores[ended]
+        flat = cand.reshape(-1)
+        pick = np.argsort(-flat, kind="stable")[:n]  # best first, ties to the lower flat index
+        top = flat[pick]
+        parent, token = pick // cand.shape[1], pick % cand.shape[1]
+        out, ended, scores = out[parent].copy(), ended[parent].copy(), scores[parent].copy()
+        caches = [[(k.clone(), v.clone()) for k, v in caches[p]] for p in parent]
+        scores = np.where(ended, scores, top)
+        out[:, t] = token
+        out[ended, t] = EOS
+        ended = out[:, t] == EOS
+        if t % CHECK_EVERY == 0 and t > c + CHECK_WINDOW:
+            ended |= np.array([compression_ratio(row) > CHECK_RATIO for row in out[:, t - CHECK_WINDOW: t]])
+        if ended.all() or t == limit:
+            break
+        xs = [dec.embed(int(out[b, t])) for b in range(n)]
+        t += 1
+    return [int(v) for v in out[0, c - 1: t + 1] if v not in (PAD, BOS, EOS)]

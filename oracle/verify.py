@@ -87,6 +87,34 @@ def verify_attention(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, le
     return out
 
 
+def beam_attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, ctx_len: np.ndarray, kg: np.ndarray,
+                   vg: np.ndarray, ptr: np.ndarray, gen_len: np.ndarray, beams: int, scale: float) -> np.ndarray:
+    """Beam attention in float64: row r = g*beams + i over the first ctx_len[g] keys of context row g, then its
+    generated keys j < gen_len[r], key j taken from row ptr[r, j] of kg / vg; no key at all gives zeros.
+    (src/omniasr_trt/kernels.py:309-332: ``_beam_ctx`` with CAUSAL=False, ``_beam_gen``, ``_beam_combine``.)
+    Pinned by: one beam with no generated keys is verify_attention at T = 1; context-free rows whose pointers all
+    name the row itself are verify_attention over that row of kg; a gather-then-softmax restatement on small
+    inputs (tests/test_oracle.py)."""
+    rows, heads, d = q.shape
+    out = np.zeros((rows, heads, d), dtype=np.float64)
+    for r in range(rows):
+        g = r // beams
+        nc = int(min(max(int(ctx_len[g]), 0), kc.shape[2]))
+        ng = int(min(max(int(gen_len[r]), 0), kg.shape[2]))
+        if nc + ng == 0:
+            continue
+        j = np.arange(ng)
+        src = np.clip(np.asarray(ptr[r, :ng], dtype=np.int64), 0, kg.shape[0] - 1)
+        k = np.concatenate([np.asarray(kc[g, :, :nc], dtype=np.float64),
+                            np.asarray(kg[src, :, j], dtype=np.float64).transpose(1, 0, 2)], 1)  # [H, L, D]
+        v = np.concatenate([np.asarray(vc[g, :, :nc], dtype=np.float64),
+                            np.asarray(vg[src, :, j], dtype=np.float64).transpose(1, 0, 2)], 1)
+        sc = np.einsum("hd,hld->hl", np.asarray(q[r], dtype=np.float64), k, optimize=True) * scale
+        w = np.exp(sc - sc.max(-1, keepdims=True))
+        out[r] = np.einsum("hl,hld->hd", w, v, optimize=True) / w.sum(-1, keepdims=True)
+    return out
+
+
 # ---------------------------------------------------------------------------------------------- argmax
 
 def log_softmax_f32(logits: np.ndarray, lse_shift: int = 0) -> np.ndarray:

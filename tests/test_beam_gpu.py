@@ -1,0 +1,178 @@
+"""Beam search on the HIP kernels: ``beam_attention`` against the oracle (fp64), and ``BeamDecoder`` against the
+reference-order beam loop on small random fp32 models (src tests/test_beam.py, tests/test_kernels.py:98-147)."""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference as oref
+from oracle import verify as ov
+from omniasr_trt_amd import beam, decode, kernels, llm
+from omniasr_trt_amd.beam import BeamDecoder
+from omniasr_trt_amd.decode import GreedyDecoder
+
+from test_decode_gpu import contexts, gpu_pair
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = (2e-2, 1e-2)
+F32_TOL = (1e-4, 1e-4)
+
+
+def say(*a):
+    print(*a, flush=True, file=sys.stderr)
+
+
+def npf(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def _beam_inputs(dtype, groups, beams, h, d, cap, gcap, ctx_len, gen_len, seed):
+    g = torch.Generator().manual_seed(seed)
+    rows = groups * beams
+    kc = torch.randn(groups + 1, h, cap, d, generator=g).to(dtype)
+    vc = torch.randn(groups + 1, h, cap, d, generator=g).to(dtype)
+    kg = torch.randn(rows + 2, h, gcap, d, generator=g).to(dtype)
+    vg = torch.randn(rows + 2, h, gcap, d, generator=g).to(dtype)
+    q = torch.randn(rows, h, d, generator=g).to(dtype)
+    ptr = torch.randint(0, rows + 2, (rows, gcap), generator=g, dtype=torch.int32)
+    return q, kc, vc, kg, vg, ptr, torch.as_tensor(ctx_len), torch.as_tensor(gen_len)
+
+
+def _beam_case(cuda, dtype, groups, beams, h, d, cap, gcap, ctx_len, gen_len, ctx_keys, seed, tol, chunk=0):
+    q, kc, vc, kg, vg, ptr, cl, gl = _beam_inputs(dtype, groups, beams, h, d, cap, gcap, ctx_len, gen_len, seed)
+    say(f"beam attention dtype={dtype} groups={groups} beams={beams} h={h} d={d} ctx={cl.tolist()[:8]} "
+        f"gen_max={int(gl.max())} chunk={chunk}")
+    out = kernels.beam_attention(q.to(cuda), kc.to(cuda), vc.to(cuda), cl.to(cuda), kg.to(cuda), vg.to(cuda),
+                                 ptr.to(cuda), gl.to(cuda), beams, ctx_keys, d ** -0.5, chunk=chunk)
+    torch.cuda.synchronize()
+    want = ov.beam_attention(npf(q), npf(kc), npf(vc), cl.numpy(), npf(kg), npf(vg), ptr.numpy(), gl.numpy(), beams,
+                             d ** -0.5)
+    np.testing.assert_allclose(npf(out), want, atol=tol[0], rtol=tol[1])
+    return out
+
+
+@pytest.mark.parametrize("beams", [1, 3, 5])
+@pytest.mark.parametrize("d", [128, 64, 512])
+def test_beam_attention_bf16(cuda, beams, d):
+    """The reference's case (tests/test_kernels.py:98-126): a finished input reads nothing, ragged generated
+    lengths, pointers anywhere in the generated rows."""
+    groups = 4
+    gen_len = torch.randint(0, 300, (groups * beams,), generator=torch.Generator().manual_seed(beams))
+    gen_len[-beams:] = 0
+    out = _beam_case(cuda, torch.bfloat16, groups, beams, 8, d, 600, 300, [600, 333, 1, 0], gen_len, 640, 9,
+                     BF16_TOL)
+    assert torch.all(out[-beams:] == 0)
+
+
+@pytest.mark.parametrize("beams", [1, 4])
+@pytest.mark.parametrize("d", [16, 512])
+def test_beam_attention_f32(cuda, beams, d):
+    gen_len = torch.randint(0, 70, (3 * beams,), generator=torch.Generator().manual_seed(d))
+    _beam_case(cuda, torch.float32, 3, beams, 2, d, 300, 70, [300, 65, 0], gen_len, 320, 10, F32_TOL)
+
+
+def test_beam_attention_config5(cuda):
+    """Config 5 (beam variant): 8 inputs x 5 beams, 32 heads x 128, contexts U[750, 2400], 1-160 generated keys;
+    several split sizes."""
+    g = torch.Generator().manual_seed(55)
+    ctx_len = torch.randint(750, 2401, (8,), generator=g)
+    gen_len = torch.randint(1, 161, (40,), generator=g)
+    keys = -(-int(ctx_len.max()) // 256) * 256
+    for chunk in (0, 64, 256):
+        _beam_case(cuda, torch.bfloat16, 8, 5, 32, 128, keys, 256, ctx_len, gen_len, keys, 56, BF16_TOL, chunk=chunk)
+
+
+def test_beam_attention_graph_replays(cuda):
+    """Captured once, replayed with new pointers and lengths written in place between replays."""
+    q, kc, vc, kg, vg, ptr, cl, gl = _beam_inputs(torch.bfloat16, 4, 3, 8, 128, 512, 128, [500, 200, 37, 512],
+                                                  [5, 0, 17, 128, 64, 1, 9, 3, 100, 2, 0, 77], 12)
+    q, kc, vc, kg, vg, ptr, cl, gl = (t.to(cuda) for t in (q, kc, vc, kg, vg, ptr, cl, gl))
+    kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr, gl, 3, 512, 128 ** -0.5)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        graph.capture_begin()
+        out = kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr, gl, 3, 512, 128 ** -0.5)
+        graph.capture_end()
+    torch.cuda.current_stream().wait_stream(stream)
+    g = torch.Generator(device=cuda).manual_seed(3)
+    for rep in range(4):
+        ptr.copy_(torch.randint(0, 14, ptr.shape, device=cuda, generator=g, dtype=torch.int32))
+        gl.copy_(torch.randint(0, 129, gl.shape, device=cuda, generator=g))
+        cl.copy_(torch.randint(0, 513, cl.shape, device=cuda, generator=g))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr, gl, 3, 512, 128 ** -0.5)
+        assert torch.equal(out, eager), rep
+
+
+def test_beam_attention_rejects_bad_shapes(cuda):
+    q, kc, vc, kg, vg, ptr, cl, gl = (t.to(cuda) for t in _beam_inputs(torch.bfloat16, 2, 2, 2, 64, 64, 16,
+                                                                       [4, 4], [1, 1, 1, 1], 0))
+    with pytest.raises(ValueError):
+        kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr[:, :8], gl, 2, 64, 0.125)  # fewer pointers than positions
+    with pytest.raises(ValueError):
+        kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr.long(), gl, 2, 64, 0.125)
+    with pytest.raises(kernels._lib.KernelError):
+        kernels.beam_attention(q[:2].repeat(9, 1, 1), kc, vc, torch.zeros(1, dtype=torch.long, device=cuda),
+                               kg.repeat(5, 1, 1, 1), vg.repeat(5, 1, 1, 1), ptr.repeat(5, 1), gl.repeat(5), 18, 64,
+                               0.125)  # 18 beams: more queries than the kernel takes
+
+
+# ---------------------------------------------------------------------------------------------- the decoder
+
+@pytest.mark.parametrize("beams,length_norm", [(2, False), (5, False), (5, True), (3, True)])
+def test_beam_decoder_matches_reference_order(cuda, beams, length_norm):
+    m, ref_dec = gpu_pair(12)
+    ctxs = contexts(2, (6, 40, 13, 25, 9))
+    ref = [oref.beam_reference(ref_dec, c, beams, length_norm) for c in ctxs]
+    assert len({tuple(r) for r in ref}) > 1
+    for graphs in (False, True):
+        say(f"beam decoder beams={beams} length_norm={length_norm} graphs={graphs}")
+        # fewer groups than inputs: a finished group takes the next input
+        dec = BeamDecoder(m, beams=beams, length_norm=length_norm, max_batch=2, sync_every=5, graphs=graphs,
+                          reserve=16)
+        assert dec.generate([c.cuda() for c in ctxs]) == ref
+        assert dec.generate([c.cuda() for c in ctxs[:2]]) == ref[:2]
+
+
+def test_one_beam_is_the_greedy_decoder(cuda):
+    m, ref_dec = gpu_pair(11)
+    ctxs = [c.cuda() for c in contexts(1, (5, 30, 17))]
+    want = GreedyDecoder(m, max_batch=3, sync_every=4, reserve=16).generate(ctxs)
+    assert BeamDecoder(m, beams=1, max_batch=2, sync_every=4, reserve=16).generate(ctxs) == want
+    assert want == [oref.greedy_reference(ref_dec, c.cpu()) for c in ctxs]
+
+
+@pytest.mark.parametrize("beams,length_norm", [(3, False), (4, True)])
+def test_repetition_stop_lands_on_the_same_step(cuda, monkeypatch, beams, length_norm):
+    """EOS made impossible: decoding ends by the repetition stop (or the position cap), which must fire at the
+    step it fires in the reference loop; more than 256 generated positions grow the caches, which are released
+    at the end of the call."""
+    monkeypatch.setattr(beam, "LIMIT", 700)
+    m, ref_dec = gpu_pair(15, edit=lambda m: m.final_proj.weight.data[llm.EOS].zero_())
+    ctxs = contexts(4, (5, 60, 140, 151, 30, 99))  # checks at positions 250 and 500 from different contexts
+    ref = [oref.beam_reference(ref_dec, c, beams, length_norm, limit=700) for c in ctxs]
+    dec = BeamDecoder(m, beams=beams, length_norm=length_norm, max_batch=3, sync_every=7, reserve=64)
+    dec.context_floor = 0
+    say(f"repetition stop beams={beams} length_norm={length_norm}")
+    assert dec.generate([c.cuda() for c in ctxs]) == ref
+    assert dec.stats["repetition_stops"] >= 1
+    assert dec.stats["grows"] >= 1 and dec.ccap == dec.gcap == 0
+    assert dec.generate([ctxs[0].cuda()]) == ref[:1]
+
+
+def test_position_cap(cuda, monkeypatch):
+    monkeypatch.setattr(beam, "LIMIT", 40)
+    m, ref_dec = gpu_pair(23, edit=lambda m: m.final_proj.weight.data[llm.EOS].mul_(0.3))
+    ctxs = contexts(24, (5, 30, 39, 41, 12))
+    ref = [oref.beam_reference(ref_dec, c, 3, False, limit=40) for c in ctxs]
+    dec = BeamDecoder(m, beams=3, max_batch=2, sync_every=4, reserve=16)
+    assert dec.generate([c.cuda() for c in ctxs]) == ref
+    assert decode.LIMIT != 40  # only the beam module's cap was changed

@@ -166,6 +166,54 @@ def test_one_query_is_decode_attention():
         np.testing.assert_allclose(out[r], (ref @ torch.from_numpy(vc[r, :, :n]))[:, 0].numpy(), rtol=1e-12)
 
 
+def _beam_case(seed, groups=3, beams=2, heads=2, d=8, cap=20, gcap=9):
+    rng = np.random.default_rng(seed)
+    rows = groups * beams
+    q = rng.standard_normal((rows, heads, d))
+    kc, vc = rng.standard_normal((2, groups + 1, heads, cap, d))
+    kg, vg = rng.standard_normal((2, rows + 2, heads, gcap, d))
+    ptr = rng.integers(0, rows + 2, (rows, gcap)).astype(np.int32)
+    return q, kc, vc, kg, vg, ptr
+
+
+def test_beam_attention_reductions():
+    """One beam without generated keys is decode attention; context-free rows whose pointers name themselves are
+    decode attention over their own generated rows."""
+    q, kc, vc, kg, vg, ptr = _beam_case(7, beams=1)
+    ctx_len = np.array([20, 4, 0])
+    out = ov.beam_attention(q, kc, vc, ctx_len, kg, vg, ptr, np.zeros(3, np.int64), 1, 0.3)
+    np.testing.assert_allclose(out, ov.verify_attention(q, kc, vc, ctx_len, 1, 0.3), rtol=1e-12, atol=1e-15)
+    q, kc, vc, kg, vg, ptr = _beam_case(8, beams=3)
+    rows = q.shape[0]
+    own = np.repeat(np.arange(rows, dtype=np.int32)[:, None], ptr.shape[1], 1)
+    gen_len = np.array([9, 1, 0, 5, 3, 7, 2, 8, 4])
+    out = ov.beam_attention(q, kc, vc, np.zeros(3, np.int64), kg, vg, own, gen_len, 3, 0.3)
+    want = ov.verify_attention(q, kg[:rows], vg[:rows], gen_len, 1, 0.3)
+    np.testing.assert_allclose(out, want, rtol=1e-12, atol=1e-15)
+
+
+def test_beam_attention_is_gather_then_masked_softmax():
+    """The unfused formulation: every row gathers its full context and generated caches, masks what it may not see
+    and takes one softmax (src/omniasr_trt/beam.py:113-125), in torch float64."""
+    q, kc, vc, kg, vg, ptr = _beam_case(9, groups=4, beams=3)
+    ctx_len = np.array([20, 13, 1, 0])
+    gen_len = np.array([9, 0, 4, 6, 2, 1, 0, 9, 3, 0, 0, 0])
+    out = ov.beam_attention(q, kc, vc, ctx_len, kg, vg, ptr, gen_len, 3, 0.3)
+    t = {k: torch.from_numpy(v) for k, v in dict(q=q, kc=kc, vc=vc, kg=kg, vg=vg).items()}
+    rows, cap, gcap = q.shape[0], kc.shape[2], kg.shape[2]
+    group = torch.arange(rows) // 3
+    src = torch.from_numpy(ptr).long()
+    j = torch.arange(gcap)
+    k = torch.cat([t["kc"][group], t["kg"][src, :, j].transpose(1, 2)], 2)  # [R, H, C + G, D]
+    v = torch.cat([t["vc"][group], t["vg"][src, :, j].transpose(1, 2)], 2)
+    allowed = torch.cat([torch.arange(cap)[None] < torch.from_numpy(ctx_len)[group, None],
+                         j[None] < torch.from_numpy(gen_len)[:, None]], 1)
+    sc = (t["q"][:, :, None, :] @ k.transpose(-1, -2)) * 0.3
+    w = torch.softmax(sc.masked_fill(~allowed[:, None, None], float("-inf")), -1).nan_to_num(0.0)
+    np.testing.assert_allclose(out, (w @ v)[:, :, 0].numpy(), rtol=1e-12, atol=1e-14)
+    assert np.all(out[9:] == 0)  # the finished group reads nothing
+
+
 # ---------------------------------------------------------------------------------------------- argmax
 
 def test_argmax_oracle_matches_torch_log_softmax():
@@ -367,3 +415,60 @@ def test_early_stop_rule_known_answers():
     assert llm.early_stop_index(out, 240, 600, ctx=300) == 500
     assert llm.early_stop_index(out, 240, 499, ctx=300) is None
     assert llm.early_stop_index(out, 240, 800, ctx=420) == 750
+
+
+# ---------------------------------------------------------------------------------------------- beam search
+
+def _small_decoder(seed, vocab=12, peak=4.0):
+    from omniasr_trt_amd.modeling import DecoderConfig, DecoderModel
+
+    torch.manual_seed(seed)
+    cfg = DecoderConfig(model_dim=32, num_layers=2, num_heads=2, ffn_dim=24, vocab_size=vocab, num_langs=5,
+                        max_seq_len=512)
+    m = DecoderModel(cfg).double().eval()
+    with torch.no_grad():
+        for p in m.parameters():
+            p.normal_(0, 0.5)
+        m.final_proj.weight.mul_(peak)
+    return oref.Fp64Decoder(m)
+
+
+def _contexts(seed, lengths):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(n, 32, generator=g, dtype=torch.float64) for n in lengths]
+
+
+def test_one_beam_is_greedy():
+    dec = _small_decoder(11)
+    for c in _contexts(1, (5, 30, 17)):
+        greedy = oref.greedy_reference(dec, c)
+        assert oref.beam_reference(dec, c, 1) == greedy
+        assert oref.beam_reference(dec, c, 1, length_norm=True) == greedy  # a monotone map of one row's offers
+
+
+def test_beam_search_two_tokens_brute_force():
+    """As many beams as tokens, stopped after two tokens: every first token survives the first step, so the result is
+    the best of all two-token sequences (a sequence that starts with EOS keeps EOS's score)."""
+    dec = _small_decoder(13, peak=1.0)  # flatter distributions: greedy misses the best pair in 4 of these 10
+    vocab = dec.sd["final_proj.weight"].size(0)
+    differs = 0
+    for c in _contexts(2, (6, 11, 3, 25, 9, 14, 7, 8, 19, 4)):
+        n = c.size(0)
+        cache = [None] * dec.layers
+        dec.forward(c[: n - 1], torch.arange(n - 1), cache)
+        lp1 = F.log_softmax(dec.logits(dec.forward(c[n - 1][None], torch.tensor([n - 1]), cache)[0]), -1)
+        best, best_seq = -math.inf, None
+        for a in range(vocab):
+            if a == oref.EOS:
+                score, seq = float(lp1[a]), (a, oref.EOS)
+            else:
+                branch = [(k.clone(), v.clone()) for k, v in cache]
+                lp2 = F.log_softmax(dec.logits(dec.forward(dec.embed(a)[None], torch.tensor([n]), branch)[0]), -1)
+                b = int(lp2.argmax())
+                score, seq = float(lp1[a] + lp2[b]), (a, b)
+            if score > best:
+                best, best_seq = score, seq
+        want = [t for t in best_seq if t not in (oref.PAD, oref.BOS, oref.EOS)]
+        assert oref.beam_reference(dec, c, vocab, limit=n) == want
+        differs += oref.greedy_reference(dec, c, limit=n) != want
+    assert differs >= 2  # the search found sequences greedy decoding misses
