@@ -7,6 +7,7 @@ A drop-in for omniasr-trt's decode-step kernels (``omniasr_trt.kernels``) and th
   argmax + acceptance / rollback;
 * ``decode``   -- ``GreedyDecoder``: static KV cache, HIP-graph steps, continuous-batching host loop;
 * ``spec``     -- ``SpecDecoder``: the drafted (speculative) greedy step;
+* ``beam``     -- ``BeamDecoder``: batched beam search over shared-context / pointer-indirected caches;
 * ``modeling`` -- the omniASR LLM decoder (fairseq2 parameter names) and its RoPE table;
 * ``llm``      -- streaming constants, the repetition stop, CTC-frame drafts.
 
@@ -21,9 +22,10 @@ _sys.modules.setdefault(_ALIAS, _sys.modules[__name__])
 
 from . import _lib, kernels, llm, modeling  # noqa: E402
 from . import decode, spec  # noqa: E402
+from . import beam  # noqa: E402
 
 for _name, _mod in (("_lib", _lib), ("kernels", kernels), ("llm", llm), ("modeling", modeling), ("decode", decode),
-                    ("spec", spec)):
+                    ("spec", spec), ("beam", beam)):
     _sys.modules.setdefault(f"{_ALIAS}.{_name}", _mod)
 
-__all__ = ["decode", "kernels", "llm", "modeling", "spec"]
+__all__ = ["beam", "decode", "kernels", "llm", "modeling", "spec"]

@@ -10,6 +10,7 @@ omniASR decoder's parameter names; nothing else of the product is used.
 
 from __future__ import annotations
 
+import math
 import zlib
 
 import numpy as np
@@ -120,7 +121,7 @@ def greedy_reference(dec: Fp64Decoder, ctx: torch.Tensor, limit: int = MAX_GEN -
 
 @torch.inference_mode()
 def beam_reference(dec: Fp64Decoder, ctx: torch.Tensor, beams: int, length_norm: bool = False,
-                   limit: int = MAX_GEN - 4) -> list[int]:
+                   limit: int = MAX_GEN - 4, margins: list | None = None) -> list[int]:
     """Beam search of one context [C, D] in the reference's order of computation (src/omniasr_trt/llm.py:205-254).
 
     ``beams`` hypotheses, each with its own K/V cache; at the first step only hypothesis 0 is live (the others
@@ -131,6 +132,10 @@ def beam_reference(dec: Fp64Decoder, ctx: torch.Tensor, beams: int, length_norm:
     hypotheses whose last 100 tokens compress more than 4x at the checked positions.  The text is hypothesis 0's.
     Pinned by: one beam is ``greedy_reference``; with as many beams as tokens and a stop after two tokens, the
     result is the best of all two-token sequences by brute force (tests/test_oracle.py).
+
+    ``margins``: if a list, receives per step the smallest gap between consecutive offers among the best
+    ``beams`` + 1 finite ones (relative to their size): where it is tiny, another rounding of the same arithmetic
+    can choose other survivors or order them differently.
     """
     ctx = ctx.detach().to("cpu", torch.float64)
     c, n = ctx.size(0), beams
@@ -156,8 +161,14 @@ def beam_reference(dec: Fp64Decoder, ctx: torch.Tensor, beams: int, length_norm:
         cand[ended] = -np.inf
         cand[ended, EOS] = scores[ended]
         flat = cand.reshape(-1)
-        pick = np.argsort(-flat, kind="stable")[:n]  # best first, ties to the lower flat index
+        order = np.argsort(-flat, kind="stable")  # best first, ties to the lower flat index
+        pick = order[:n]
         top = flat[pick]
+        if margins is not None:
+            best = flat[order[: n + 1]]
+            best = best[np.isfinite(best)]
+            gaps = np.abs(np.diff(best)) / np.maximum(np.abs(best[1:]), 1.0)
+            margins.append(float(gaps.min()) if gaps.size else math.inf)
         parent, token = pick // cand.shape[1], pick % cand.shape[1]
         out, ended, scores = out[parent].copy(), ended[parent].copy(), scores[parent].copy()
         caches = [[(k.clone(), v.clone()) for k, v in caches[p]] for p in parent]

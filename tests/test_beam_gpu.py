@@ -9,7 +9,7 @@ import torch
 
 from oracle import reference as oref
 from oracle import verify as ov
-from omniasr_trt_amd import beam, decode, kernels, llm
+from omniasr_trt_amd import beam, kernels, llm
 from omniasr_trt_amd.beam import BeamDecoder
 from omniasr_trt_amd.decode import GreedyDecoder
 
@@ -127,11 +127,32 @@ def test_beam_attention_rejects_bad_shapes(cuda):
 
 # ---------------------------------------------------------------------------------------------- the decoder
 
+# A beam search compares sums of log-probabilities across hypotheses: where two offers at the survivors' boundary
+# (or two survivors) are closer than the difference between fp32 and fp64 arithmetic, both choices are correct
+# roundings of the same search.  The fixtures below are contexts whose oracle run has no such near-tie (every gap
+# among the best beams + 1 offers above ROBUST, relative), so the HIP path must give exactly the reference's tokens.
+ROBUST = 2e-5
+
+
+def picked(picks, lengths):
+    """Context i of ``contexts(seed, lengths)`` for each (seed, i)."""
+    return [contexts(seed, lengths)[i] for seed, i in picks]
+
+
+def references(ref_dec, ctxs, beams, length_norm, **kw):
+    out = []
+    for c in ctxs:
+        margins = []
+        out.append(oref.beam_reference(ref_dec, c, beams, length_norm, margins=margins, **kw))
+        assert min(margins) > ROBUST, f"fixture of length {c.size(0)} has a near-tie ({min(margins):.1e})"
+    return out
+
+
 @pytest.mark.parametrize("beams,length_norm", [(2, False), (5, False), (5, True), (3, True)])
 def test_beam_decoder_matches_reference_order(cuda, beams, length_norm):
     m, ref_dec = gpu_pair(12)
-    ctxs = contexts(2, (6, 40, 13, 25, 9))
-    ref = [oref.beam_reference(ref_dec, c, beams, length_norm) for c in ctxs]
+    ctxs = picked(((5, 2), (13, 0), (13, 1), (11, 3), (9, 4), (6, 2), (10, 1)), (6, 40, 13, 25, 9))
+    ref = references(ref_dec, ctxs, beams, length_norm)
     assert len({tuple(r) for r in ref}) > 1
     for graphs in (False, True):
         say(f"beam decoder beams={beams} length_norm={length_norm} graphs={graphs}")
@@ -140,6 +161,16 @@ def test_beam_decoder_matches_reference_order(cuda, beams, length_norm):
                           reserve=16)
         assert dec.generate([c.cuda() for c in ctxs]) == ref
         assert dec.generate([c.cuda() for c in ctxs[:2]]) == ref[:2]
+
+
+def test_beam_changes_the_result(cuda):
+    """The fixtures are not all decided greedily: beam search picks other texts for some of them."""
+    m, ref_dec = gpu_pair(12)
+    ctxs = picked(((5, 2), (13, 0), (13, 1), (11, 3)), (6, 40, 13, 25, 9))
+    greedy = GreedyDecoder(m, max_batch=2, sync_every=5, reserve=16).generate([c.cuda() for c in ctxs])
+    beams = BeamDecoder(m, beams=5, max_batch=2, sync_every=5, reserve=16).generate([c.cuda() for c in ctxs])
+    assert beams == references(ref_dec, ctxs, 5, False)
+    assert sum(g != b for g, b in zip(greedy, beams)) >= 2
 
 
 def test_one_beam_is_the_greedy_decoder(cuda):
@@ -152,14 +183,16 @@ def test_one_beam_is_the_greedy_decoder(cuda):
 
 @pytest.mark.parametrize("beams,length_norm", [(3, False), (4, True)])
 def test_repetition_stop_lands_on_the_same_step(cuda, monkeypatch, beams, length_norm):
-    """EOS made impossible: decoding ends by the repetition stop (or the position cap), which must fire at the
-    step it fires in the reference loop; more than 256 generated positions grow the caches, which are released
-    at the end of the call."""
+    """EOS logit zeroed (the others are peaked): hypotheses loop until the repetition stop ends them at a checked
+    position, which must happen at the step it happens in the reference loop.  Buckets of 32 positions: the
+    generated caches grow every few host looks and the context caches when a longer context arrives; the grown
+    caches are released at the end of the call."""
     monkeypatch.setattr(beam, "LIMIT", 700)
+    monkeypatch.setattr(beam, "KEY_BUCKET", 32)
     m, ref_dec = gpu_pair(15, edit=lambda m: m.final_proj.weight.data[llm.EOS].zero_())
-    ctxs = contexts(4, (5, 60, 140, 151, 30, 99))  # checks at positions 250 and 500 from different contexts
-    ref = [oref.beam_reference(ref_dec, c, beams, length_norm, limit=700) for c in ctxs]
-    dec = BeamDecoder(m, beams=beams, length_norm=length_norm, max_batch=3, sync_every=7, reserve=64)
+    ctxs = picked(((8, 5), (10, 2), (10, 6), (9, 5), (7, 2), (11, 4)), (5, 60, 140, 151, 30, 99, 20, 120))
+    ref = references(ref_dec, ctxs, beams, length_norm, limit=700)
+    dec = BeamDecoder(m, beams=beams, length_norm=length_norm, max_batch=3, sync_every=7, reserve=16)
     dec.context_floor = 0
     say(f"repetition stop beams={beams} length_norm={length_norm}")
     assert dec.generate([c.cuda() for c in ctxs]) == ref
@@ -172,7 +205,7 @@ def test_position_cap(cuda, monkeypatch):
     monkeypatch.setattr(beam, "LIMIT", 40)
     m, ref_dec = gpu_pair(23, edit=lambda m: m.final_proj.weight.data[llm.EOS].mul_(0.3))
     ctxs = contexts(24, (5, 30, 39, 41, 12))
-    ref = [oref.beam_reference(ref_dec, c, 3, False, limit=40) for c in ctxs]
+    ref = references(ref_dec, ctxs, 3, False, limit=40)
     dec = BeamDecoder(m, beams=3, max_batch=2, sync_every=4, reserve=16)
     assert dec.generate([c.cuda() for c in ctxs]) == ref
-    assert decode.LIMIT != 40  # only the beam module's cap was changed
+    assert [len(r) for r in ref][2:4] == [3, 1]  # contexts ending at the cap: three tokens, and the first only
