@@ -91,29 +91,44 @@ __device__ __forceinline__ void store4<uint16_t>(uint16_t* p, f32x4_t v) {
   *reinterpret_cast<uint2*>(p) = w;
 }
 
+// The in-kernel merge reads partials written by waves on other XCDs, whose L2s are not coherent with each other.
+// Those partials are stored and loaded with agent-scope (relaxed atomic) accesses, which go through the L2 to the
+// device's coherence point: no L2 writeback or invalidate of the whole cache is needed, only the wave's own stores
+// completing before its ticket.
+__device__ __forceinline__ void put_partial(float* p, float v, bool through) {
+  if (through) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *p = v;
+}
+
+__device__ __forceinline__ float get_through(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Partial slot of the q-th partial to merge: the row's key splits, then the generated-keys slot if any.
 __device__ __forceinline__ int merge_slot(const AttnArgs& a, int nact, int q) {
   return q < nact ? q : a.gen_split;
 }
 
-// Log-sum-exp merge of the partials of (row b, head h) by one wave; writes the output.
-template <typename OutT>
+// Log-sum-exp merge of the partials of (row b, head h) by one wave; writes the output.  THROUGH: the partials are
+// read at the coherence point (in-kernel merge).
+template <typename OutT, bool THROUGH>
 __device__ void merge_splits(const AttnArgs& a, int b, int h, int nact) {
   const int lane = lane_id();
   const int nq = nact + (a.gen_split >= 0 ? 1 : 0);
   const int64_t split0 = ((int64_t)b * a.H + h) * a.splits;
   OutT* out = reinterpret_cast<OutT*>(a.out);
+  auto get = [](const float* p) { return THROUGH ? get_through(p) : *p; };
   for (int t = 0; t < a.T; ++t) {
     float top = -INFINITY;
     for (int q = lane; q < nq; q += kWave)
-      top = fmaxf(top, a.part_ml[((split0 + merge_slot(a, nact, q)) * a.T + t) * 2]);
+      top = fmaxf(top, get(a.part_ml + ((split0 + merge_slot(a, nact, q)) * a.T + t) * 2));
     top = wave_max(top);
     float den = 0.f;
     for (int q = lane; q < nq; q += kWave) {
       const int64_t ml = ((split0 + merge_slot(a, nact, q)) * a.T + t) * 2;
-      const float m = a.part_ml[ml];
+      const float m = get(a.part_ml + ml);
       const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - top);
-      den += w * a.part_ml[ml + 1];
+      den += w * get(a.part_ml + ml + 1);
     }
     den = wave_sum(den);
     const float div = den > 0.f ? den : 1.f;
@@ -122,9 +137,15 @@ __device__ void merge_splits(const AttnArgs& a, int b, int h, int nact) {
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
       for (int q = 0; q < nq; ++q) {
         const int64_t slot = (split0 + merge_slot(a, nact, q)) * a.T + t;
-        const float m = a.part_ml[slot * 2];
+        const float m = get(a.part_ml + slot * 2);
         const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - top);
-        const f32x4_t po = *reinterpret_cast<const f32x4_t*>(a.part_o + slot * a.D + d);
+        const float* src = a.part_o + slot * a.D + d;
+        f32x4_t po;
+        if constexpr (THROUGH) {
+          po = f32x4_t{get_through(src), get_through(src + 1), get_through(src + 2), get_through(src + 3)};
+        } else {
+          po = *reinterpret_cast<const f32x4_t*>(src);
+        }
         acc += w * po;
       }
       store4<OutT>(orow + d, acc / div);
@@ -136,16 +157,18 @@ __device__ void merge_splits(const AttnArgs& a, int b, int h, int nact) {
 template <typename OutT>
 __device__ __forceinline__ void finish_split(const AttnArgs& a, int b, int h, int nact) {
   if (a.separate) return;
-  // Release at agent scope: this wave's partial leaves its XCD's L2 before the ticket is taken
-  // (the L2s of the 8 XCDs are not coherent with each other).
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  // This wave's partial stores (agent scope, written through) have reached the coherence point before its ticket
+  // is taken; the compiler barriers keep them on their side of the wait.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  int* counter = &a.counters[b * a.H + h];
   int ticket = 0;
-  if (lane_id() == 0) ticket = atomicAdd(&a.counters[b * a.H + h], 1);
+  if (lane_id() == 0) ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   ticket = __shfl(ticket, 0, kWave);
   if (ticket != nact - 1) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the other splits' partials, not stale lines
-  merge_splits<OutT>(a, b, h, nact);
-  if (lane_id() == 0) a.counters[b * a.H + h] = 0;  // every split of this (row, head) has arrived
+  merge_splits<OutT, true>(a, b, h, nact);  // the other splits' partials, read at the coherence point
+  if (lane_id() == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------------------------- MFMA
@@ -166,51 +189,33 @@ struct KVTile {
   u32x4_t v[NG][8];
 };
 
-// Per-lane byte offsets of a tile's elements from the tile's first key (constant over the loop).
-struct TileOffsets {
-  uint32_t k0, k1;   // K rows of MFMA blocks 0 and 1
-  uint32_t v[8];     // V rows kb + 8g + j
-};
-
 __device__ __forceinline__ u32x4_t ld16(const char* p) { return *reinterpret_cast<const u32x4_t*>(p); }
 
-// A full tile: the wave-uniform tile base (scalar registers) plus the lane's constant offsets.
+// One 32-key tile of K and V into MFMA operand layout.  Key rows are contiguous (D elements apart), so each load is
+// the wave-uniform tile base plus a 32-bit lane offset.  K rows past ``kmax`` (the last cache position, relative to
+// the tile's first key; 31 inside the cache) are read at kmax, and V rows at or past ``vstop`` (the end of the keys
+// in use, relative; 32 for a full tile) are zero, so stale memory never reaches the P V product.
 template <int D>
-__device__ __forceinline__ void load_tile(KVTile<D>& t, const char* kt, const char* vt, const TileOffsets& o) {
-#pragma unroll
-  for (int s = 0; s < KVTile<D>::KS; ++s) {
-    t.k[0][s] = ld16(kt + o.k0 + s * 64);
-    t.k[1][s] = ld16(kt + o.k1 + s * 64);
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-#pragma unroll
-    for (int gg = 0; gg < KVTile<D>::NG; ++gg) t.v[gg][j] = ld16(vt + o.v[j] + gg * 256);
-  }
-}
-
-// The last tile of a split: keys past the cache end are read at the last position and V past ``stop`` is zeroed
-// (0 * anything stays 0 in the PV product; those keys are masked out of the softmax).
-template <int D>
-__device__ __forceinline__ void load_tail_tile(KVTile<D>& t, const uint16_t* kbase, const uint16_t* vbase,
-                                               int64_t kb, int64_t stop, int64_t last_key, int64_t s_pos, int c,
-                                               int g) {
+__device__ __forceinline__ void load_tile_clamped(KVTile<D>& t, const char* kt, const char* vt, int kmax, int vstop,
+                                                  int c, int g) {
+  constexpr uint32_t kRow = D * 2;
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb) {
-    int64_t key = kb + 8 * (c >> 2) + 4 * mb + (c & 3);
-    key = key < last_key ? key : last_key;
-    const uint16_t* kp = kbase + key * s_pos + g * 8;
+    int rk = 8 * (c >> 2) + 4 * mb + (c & 3);
+    rk = rk < kmax ? rk : kmax;
+    const uint32_t ko = (uint32_t)rk * kRow + g * 16;
 #pragma unroll
-    for (int s = 0; s < KVTile<D>::KS; ++s) t.k[mb][s] = *reinterpret_cast<const u32x4_t*>(kp + s * 32);
+    for (int s = 0; s < KVTile<D>::KS; ++s) t.k[mb][s] = ld16(kt + ko + s * 64);
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int64_t key = kb + 8 * g + j;
-    const int64_t kl = key < last_key ? key : last_key;
-    const uint16_t* vp = vbase + kl * s_pos + c * 8;
+    const int rv = 8 * g + j;
+    const uint32_t vo = (uint32_t)(rv < kmax ? rv : kmax) * kRow + c * 16;
 #pragma unroll
-    for (int gg = 0; gg < KVTile<D>::NG; ++gg)
-      t.v[gg][j] = key < stop ? *reinterpret_cast<const u32x4_t*>(vp + gg * 128) : u32x4_t{0u, 0u, 0u, 0u};
+    for (int gg = 0; gg < KVTile<D>::NG; ++gg) {
+      const u32x4_t x = ld16(vt + vo + gg * 256);
+      t.v[gg][j] = rv < vstop ? x : u32x4_t{0u, 0u, 0u, 0u};
+    }
   }
 }
 
@@ -278,15 +283,19 @@ struct SoftmaxState {
   float l_run;  // this lane's share of query c's probability sum (relative to m_ref)
 };
 
-// A tile every query sees entirely: lazy reference max.
+// One tile: scores, the causal / end-of-row mask (key0 + j >= lim: query c does not see key j of this lane), the
+// lazy reference max, probabilities, O += P V.  The mask is a no-op on tiles every query sees whole.
 template <int D>
-__device__ __forceinline__ void attend_full(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float c_scale,
-                                            SoftmaxState& st, f32x4_t (&o)[D / 16], int g) {
+__device__ __forceinline__ void attend(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float c_scale,
+                                       SoftmaxState& st, f32x4_t (&o)[D / 16], int g, int64_t key0, int64_t lim) {
   float sv[8];
   tile_scores<D>(t, qop, sv);
   bool over = false;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) over |= sv[j] > st.thr;
+  for (int j = 0; j < 8; ++j) {
+    sv[j] = key0 + j < lim ? sv[j] : -INFINITY;
+    over |= sv[j] > st.thr;
+  }
   if (__any(over)) {
     float mx = sv[0];
 #pragma unroll
@@ -294,39 +303,11 @@ __device__ __forceinline__ void attend_full(const KVTile<D>& t, const u32x4_t (&
     mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
     mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
     const float m_new = fmaxf(st.m_ref, mx * c_scale);
-    rescale<D / 16>(st.m_ref, m_new, st.l_run, o, g);
+    rescale<D / 16>(st.m_ref, m_new == -INFINITY ? 0.f : m_new, st.l_run, o, g);
     st.m_ref = m_new;
-    st.thr = (m_new + kLazyLog2) / c_scale;
+    st.thr = m_new == -INFINITY ? -INFINITY : (m_new + kLazyLog2) / c_scale;
   }
-  float p[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], c_scale, -st.m_ref));
-    st.l_run += p[j];
-  }
-  tile_pv<D>(t, p, o);
-}
-
-// A tile reaching past some query's last key or the split's end: exact max over the visible keys.
-template <int D>
-__device__ __forceinline__ void attend_masked(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float c_scale,
-                                              SoftmaxState& st, f32x4_t (&o)[D / 16], int g, int64_t key0,
-                                              int64_t lim) {
-  float sv[8];
-  tile_scores<D>(t, qop, sv);
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    if (key0 + j >= lim) sv[j] = -INFINITY;
-  float mx = sv[0];
-#pragma unroll
-  for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sv[j]);
-  mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-  const float m_new = fmaxf(st.m_ref, mx * c_scale);
-  const float m_use = m_new == -INFINITY ? 0.f : m_new;
-  rescale<D / 16>(st.m_ref, m_use, st.l_run, o, g);
-  st.m_ref = m_new;
-  st.thr = m_new == -INFINITY ? -INFINITY : (m_new + kLazyLog2) / c_scale;
+  const float m_use = st.m_ref == -INFINITY ? 0.f : st.m_ref;  // no key seen yet: every probability is 0
   float p[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -336,7 +317,7 @@ __device__ __forceinline__ void attend_masked(const KVTile<D>& t, const u32x4_t 
   tile_pv<D>(t, p, o);
 }
 
-// PIPE: the next tile's loads are issued before the current tile's math (two tiles of registers).
+// PIPE: two tiles of registers, the next tile's loads in flight during the current tile's math.
 template <int D, bool PIPE>
 __global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(AttnArgs a) {
   constexpr int KS = D / 32;  // k-steps of S^T = K Q^T
@@ -375,44 +356,54 @@ __global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(Attn
   const int64_t see_all = r.total < r.n ? r.total : r.n;
   const int64_t full_tiles = see_all >> 5;  // tiles [0, full_tiles) are full
   const int64_t nfull = full_tiles > sp ? (full_tiles - sp + r.nact - 1) / r.nact : 0;
-  const uint32_t pos_bytes = (uint32_t)(a.s_pos * 2);
-  TileOffsets off;
-  off.k0 = (uint32_t)(8 * (c >> 2) + (c & 3)) * pos_bytes + g * 16;
-  off.k1 = off.k0 + 4 * pos_bytes;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) off.v[j] = (uint32_t)(8 * g + j) * pos_bytes + c * 16;
+  // The launcher sends only caches with contiguous key rows (s_pos == D) here.
   const char* kt = reinterpret_cast<const char*>(kbase) + (int64_t)sp * 32 * a.s_pos * 2;
   const char* vt = reinterpret_cast<const char*>(vbase) + (int64_t)sp * 32 * a.s_pos * 2;
   const int64_t tile_bytes = (int64_t)r.nact * 32 * a.s_pos * 2;  // stride between this split's tiles
 
-  KVTile<D> A;
-  if constexpr (PIPE) {
-    KVTile<D> B;
-    if (nfull > 0) load_tile<D>(A, kt, vt, off);
-    for (int64_t i = 0; i < nfull; i += 2) {
-      if (i + 1 < nfull) load_tile<D>(B, kt + tile_bytes, vt + tile_bytes, off);
-      attend_full<D>(A, qop, c_scale, st, o, g);
-      if (i + 1 < nfull) {
-        if (i + 2 < nfull) load_tile<D>(A, kt + 2 * tile_bytes, vt + 2 * tile_bytes, off);
-        attend_full<D>(B, qop, c_scale, st, o, g);
-      }
-      kt += 2 * tile_bytes;
-      vt += 2 * tile_bytes;
-    }
-  } else {
-    for (int64_t i = 0; i < nfull; ++i) {
-      load_tile<D>(A, kt, vt, off);
-      attend_full<D>(A, qop, c_scale, st, o, g);
-      kt += tile_bytes;
-      vt += tile_bytes;
-    }
-  }
+  // The split's tiles in order: nfull tiles every query sees whole, then at most two reaching past some query's
+  // last key.  One branch-free loader and one attend routine serve both kinds, so the only branches around the
+  // loads are the loop's own: the wait before a tile's math then leaves the next tile's loads in flight (a load
+  // under a condition makes the compiler wait for every outstanding load where the branches join).
+  const int64_t ntail =
+      row_tiles > sp + nfull * r.nact ? (row_tiles - sp - nfull * r.nact + r.nact - 1) / r.nact : 0;
+  const int64_t ntot = nfull + ntail;
   const int64_t own = r.n + (a.causal ? c : 0);
   const int64_t lim_c = own < r.total ? own : r.total;  // query c's key limit
-  for (int64_t ti = sp + nfull * r.nact; ti < row_tiles; ti += r.nact) {  // the row's last one or two tiles
-    const int64_t kb = ti * 32;
-    load_tail_tile<D>(A, kbase, vbase, kb, r.total, last_key, a.s_pos, c, g);
-    attend_masked<D>(A, qop, c_scale, st, o, g, kb + 8 * g, lim_c);
+  auto load_k = [&](KVTile<D>& t, int64_t k) {
+    const int64_t kb = (sp + k * r.nact) * 32;  // < total <= cache_len
+    const int64_t kmax = last_key - kb, vstop = r.total - kb;
+    load_tile_clamped<D>(t, kt + k * tile_bytes, vt + k * tile_bytes, kmax < 31 ? (int)kmax : 31,
+                         vstop < 32 ? (int)vstop : 32, c, g);
+  };
+  auto attend_k = [&](const KVTile<D>& t, int64_t k) {
+    attend<D>(t, qop, c_scale, st, o, g, (sp + k * r.nact) * 32 + 8 * g, lim_c);
+  };
+  if (ntot > 0) {
+    KVTile<D> A;
+    if constexpr (PIPE) {
+      KVTile<D> B;
+      load_k(A, 0);
+      int64_t k = 0;
+      for (; k + 2 < ntot; k += 2) {
+        load_k(B, k + 1);
+        attend_k(A, k);
+        load_k(A, k + 2);
+        attend_k(B, k + 1);
+      }
+      if (k + 1 < ntot) {
+        load_k(B, k + 1);
+        attend_k(A, k);
+        attend_k(B, k + 1);
+      } else {
+        attend_k(A, k);
+      }
+    } else {
+      for (int64_t k = 0; k < ntot; ++k) {
+        load_k(A, k);
+        attend_k(A, k);
+      }
+    }
   }
 
   // ---- finish: per-query sums, then either the output or this split's partial
@@ -439,20 +430,28 @@ __global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(Attn
     return;
   }
   const int64_t base = (((int64_t)b * a.H + h) * a.splits + sp) * T;
+  const bool through = !a.separate;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = 4 * g + i;
     if (t >= T) continue;
 #pragma unroll
     for (int gg = 0; gg < NG; ++gg) {
-      f32x4_t* po = reinterpret_cast<f32x4_t*>(a.part_o + (base + t) * D + gg * 128 + c * 8);
-      po[0] = f32x4_t{o[gg * 8 + 0][i], o[gg * 8 + 1][i], o[gg * 8 + 2][i], o[gg * 8 + 3][i]};
-      po[1] = f32x4_t{o[gg * 8 + 4][i], o[gg * 8 + 5][i], o[gg * 8 + 6][i], o[gg * 8 + 7][i]};
+      float* po = a.part_o + (base + t) * D + gg * 128 + c * 8;
+      if (through) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) put_partial(po + e, o[gg * 8 + e][i], true);
+      } else {
+        reinterpret_cast<f32x4_t*>(po)[0] = f32x4_t{o[gg * 8 + 0][i], o[gg * 8 + 1][i], o[gg * 8 + 2][i],
+                                                    o[gg * 8 + 3][i]};
+        reinterpret_cast<f32x4_t*>(po)[1] = f32x4_t{o[gg * 8 + 4][i], o[gg * 8 + 5][i], o[gg * 8 + 6][i],
+                                                    o[gg * 8 + 7][i]};
+      }
     }
   }
   if (g == 0 && c < T) {
-    a.part_ml[(base + c) * 2] = st.m_ref;
-    a.part_ml[(base + c) * 2 + 1] = l_tot;
+    put_partial(a.part_ml + (base + c) * 2, st.m_ref, through);
+    put_partial(a.part_ml + (base + c) * 2 + 1, l_tot, through);
   }
   finish_split<uint16_t>(a, b, h, r.nact);
 }
@@ -563,12 +562,12 @@ __global__ __launch_bounds__(64) void verify_attn_valu_kernel(AttnArgs a) {
         else
           out[((int64_t)(b * T + t) * a.H + h) * D + d] = v;
       } else {
-        a.part_o[(base + t) * D + d] = acc[t][dd];
+        put_partial(a.part_o + (base + t) * D + d, acc[t][dd], !a.separate);
       }
     }
     if (!direct && lane == 0) {
-      a.part_ml[(base + t) * 2] = m_run[t];
-      a.part_ml[(base + t) * 2 + 1] = l_tot;
+      put_partial(a.part_ml + (base + t) * 2, m_run[t], !a.separate);
+      put_partial(a.part_ml + (base + t) * 2 + 1, l_tot, !a.separate);
     }
   }
   if (direct) return;
@@ -593,7 +592,7 @@ __global__ __launch_bounds__(64) void verify_attn_combine_kernel(AttnArgs a) {
   const int64_t split0 = ((int64_t)b * a.H + h) * a.splits;
   OutT* orow = reinterpret_cast<OutT*>(a.out) + ((int64_t)(b * T + t) * a.H + h) * D;
   if (nq > kCombineMaxSplits) {  // beyond the unrolled case: the generic merge
-    if (t == 0) merge_splits<OutT>(a, b, h, nact);
+    if (t == 0) merge_splits<OutT, false>(a, b, h, nact);
     return;
   }
   const int d0 = lane * DPL;
@@ -674,7 +673,7 @@ extern "C" size_t omni_verify_attention_workspace(int32_t rows, int32_t tokens, 
 
 // Key-split kernel and (when asked) the merge launch for filled-in arguments.
 static int launch_attention(const AttnArgs& a, int rows, int dtype, hipStream_t s) {
-  const bool mfma = dtype == OMNI_BF16 && a.D % 128 == 0;
+  const bool mfma = dtype == OMNI_BF16 && a.D % 128 == 0 && a.s_pos == a.D;  // contiguous key rows
   dim3 grid(a.ctx_splits, a.H, rows);
   if (mfma) {
     switch (a.D) {
