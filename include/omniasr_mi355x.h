@@ -40,6 +40,7 @@ extern "C" {
 
 /* verify-attention flags */
 #define OMNI_ATTN_SEPARATE_COMBINE 1 /* merge key splits in a second launch, not in the last split */
+#define OMNI_ATTN_SPLIT_K 2          /* always split-K, never one workgroup per (head, row) */
 
 /* Human-readable text of a status code (static storage). */
 const char *omni_status_string(int status);
@@ -96,8 +97,12 @@ size_t omni_verify_attention_workspace(int32_t rows, int32_t tokens, int32_t hea
  * ``workspace``: at least omni_verify_attention_workspace() bytes, 256-byte aligned, any content.
  * ``counters``: rows*heads int32, zero before the first call; every call leaves them zero (calls
  * that share them must not overlap in time).
- * bf16: head_dim a multiple of 128 runs on MFMA, any other multiple of 8 on the vector ALUs;
- * f32: vector ALUs (fp32 products).  tokens: 1..16.
+ * Decomposition: with bf16, head_dim 128, contiguous key rows (stride_pos == head_dim), tokens <= 15 and
+ * rows * heads >= 128, one workgroup of 8 waves per (head, row) merges its waves' partials in LDS (no
+ * workspace traffic, one launch, ``chunk`` unused) unless ``flags`` has OMNI_ATTN_SPLIT_K; otherwise split-K
+ * as above.
+ * bf16: head_dim a multiple of 128 (contiguous key rows) runs on MFMA, any other multiple of 8 on the vector
+ * ALUs; f32: vector ALUs (fp32 products).  tokens: 1..16.
  */
 int omni_verify_attention(const void *q, const void *k_cache, const void *v_cache,
                           int64_t stride_row, int64_t stride_head, int64_t stride_pos,

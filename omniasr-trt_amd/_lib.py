@@ -19,6 +19,7 @@ ABI_VERSION = 1
 OK = 0
 F32, BF16 = 0, 1
 ATTN_SEPARATE_COMBINE = 1
+ATTN_SPLIT_K = 2
 
 _P = c_void_p
 _SIGNATURES = {

@@ -153,6 +153,85 @@ __device__ void merge_splits(const AttnArgs& a, int b, int h, int nact) {
   }
 }
 
+// The in-kernel merge by the row's last split: lane l owns the floats f = 1024p + 256r + 4l (query f / D) of the
+// row's T x D output block, and every load of a batch of up to 8 partials x 1024 floats is in flight at once (the
+// tile registers are free by then), so a typical merge is one memory round trip.
+__device__ __forceinline__ f32x4_t get_through4(const float* p) {
+  const uint64_t lo = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t hi = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)) + 1, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+  return f32x4_t{__uint_as_float((uint32_t)lo), __uint_as_float((uint32_t)(lo >> 32)),
+                 __uint_as_float((uint32_t)hi), __uint_as_float((uint32_t)(hi >> 32))};
+}
+
+template <typename OutT>
+__device__ void merge_splits_fast(const AttnArgs& a, int b, int h, int nact) {
+  constexpr int kS = 8, kR = 3;
+  const int lane = lane_id();
+  const int T = a.T, D = a.D, nf = T * D;
+  const int nq = nact + (a.gen_split >= 0 ? 1 : 0);
+  const int64_t split0 = ((int64_t)b * a.H + h) * a.splits;
+  OutT* out = reinterpret_cast<OutT*>(a.out);
+  for (int f0 = 0; f0 < nf; f0 += kR * 256) {
+    float top[kR], den[kR];
+    f32x4_t acc[kR];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      top[r] = -INFINITY;
+      den[r] = 0.f;
+      acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int q0 = 0; q0 < nq; q0 += kS) {
+      f32x4_t ov[kS][kR];
+      float mv[kS][kR], lv[kS][kR];
+#pragma unroll
+      for (int sq = 0; sq < kS; ++sq) {
+#pragma unroll
+        for (int r = 0; r < kR; ++r) {
+          const int f = f0 + r * 256 + 4 * lane;
+          mv[sq][r] = -INFINITY;
+          lv[sq][r] = 0.f;
+          ov[sq][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          if (q0 + sq < nq && f < nf) {
+            const int t = f / D;
+            const int64_t slot = (split0 + merge_slot(a, nact, q0 + sq)) * T + t;
+            const uint64_t ml = __hip_atomic_load(reinterpret_cast<uint64_t*>(a.part_ml + slot * 2), __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+            mv[sq][r] = __uint_as_float((uint32_t)ml);
+            lv[sq][r] = __uint_as_float((uint32_t)(ml >> 32));
+            ov[sq][r] = get_through4(a.part_o + slot * D + (f - t * D));
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < kR; ++r) {
+        float t2 = top[r];
+#pragma unroll
+        for (int sq = 0; sq < kS; ++sq) t2 = fmaxf(t2, mv[sq][r]);
+        const float rs = top[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(top[r] - t2);
+        den[r] *= rs;
+        acc[r] *= rs;
+#pragma unroll
+        for (int sq = 0; sq < kS; ++sq) {
+          const float wt = mv[sq][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv[sq][r] - t2);
+          den[r] += wt * lv[sq][r];
+          acc[r] += wt * ov[sq][r];
+        }
+        top[r] = t2;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      const int f = f0 + r * 256 + 4 * lane;
+      if (f >= nf) continue;
+      const int t = f / D;
+      const float div = den[r] > 0.f ? den[r] : 1.f;
+      store4<OutT>(out + ((int64_t)(b * T + t) * a.H + h) * D + (f - t * D), acc[r] / div);
+    }
+  }
+}
+
 // After a split wrote its partial: the last of the row's ``nact`` splits merges them all.
 template <typename OutT>
 __device__ __forceinline__ void finish_split(const AttnArgs& a, int b, int h, int nact) {
@@ -167,7 +246,7 @@ __device__ __forceinline__ void finish_split(const AttnArgs& a, int b, int h, in
   if (lane_id() == 0) ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   ticket = __shfl(ticket, 0, kWave);
   if (ticket != nact - 1) return;
-  merge_splits<OutT, true>(a, b, h, nact);  // the other splits' partials, read at the coherence point
+  merge_splits_fast<OutT>(a, b, h, nact);  // every split's partial, read at the coherence point
   if (lane_id() == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -287,7 +366,7 @@ struct SoftmaxState {
 // lazy reference max, probabilities, O += P V.  The mask is a no-op on tiles every query sees whole.
 template <int D>
 __device__ __forceinline__ void attend(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float c_scale,
-                                       SoftmaxState& st, f32x4_t (&o)[D / 16], int g, int64_t key0, int64_t lim) {
+                                       SoftmaxState& st, f32x4_t (&o)[D / 16], int g, int key0, int lim) {
   float sv[8];
   tile_scores<D>(t, qop, sv);
   bool over = false;
@@ -317,15 +396,15 @@ __device__ __forceinline__ void attend(const KVTile<D>& t, const u32x4_t (&qop)[
   tile_pv<D>(t, p, o);
 }
 
+// One split's share of row b, head h: tiles sp, sp + nact, sp + 2 nact, ... of the row (r.nact splits).  Leaves
+// the split's unnormalised output rows in ``o`` and its softmax state in ``st``.
 // PIPE: two tiles of registers, the next tile's loads in flight during the current tile's math.
 template <int D, bool PIPE>
-__global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(AttnArgs a) {
+__device__ __forceinline__ void attend_split(const AttnArgs& a, int b, int h, int sp, const SplitRange& r,
+                                             SoftmaxState& st, f32x4_t (&o)[D / 16]) {
   constexpr int KS = D / 32;  // k-steps of S^T = K Q^T
   constexpr int NG = D / 128;  // 128-wide output groups
-  const int sp = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const SplitRange r = split_range(a, b, sp);
-  if (sp >= r.nact) return;
-  const int lane = threadIdx.x, c = lane & 15, g = lane >> 4;
+  const int lane = lane_id(), c = lane & 15, g = lane >> 4;
   const int T = a.T;
 
   const uint16_t* kbase = reinterpret_cast<const uint16_t*>(a.k) + b * a.s_row + h * a.s_head;
@@ -343,10 +422,9 @@ __global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(Attn
     for (int s = 0; s < KS; ++s) qop[s] = c < T ? *reinterpret_cast<const u32x4_t*>(qrow + s * 32) : zero;
   }
 
-  SoftmaxState st{-INFINITY, -INFINITY, 0.f};
-  f32x4_t o[NG * 8];  // o[8gg + e][i]: output row 4g + i, dimension 128gg + 8c + e
+  st = SoftmaxState{-INFINITY, -INFINITY, 0.f};
 #pragma unroll
-  for (int nb = 0; nb < NG * 8; ++nb) o[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int nb = 0; nb < NG * 8; ++nb) o[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};  // row 4g + i, dimension 128gg + 8c + e
 
   // The row's 32-key tiles are dealt out round-robin over its nact splits: split sp takes tiles sp, sp + nact,
   // sp + 2 nact, ...  Each split gets the same number of tiles (give or take one), and at any moment the row's
@@ -369,7 +447,7 @@ __global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(Attn
       row_tiles > sp + nfull * r.nact ? (row_tiles - sp - nfull * r.nact + r.nact - 1) / r.nact : 0;
   const int64_t ntot = nfull + ntail;
   const int64_t own = r.n + (a.causal ? c : 0);
-  const int64_t lim_c = own < r.total ? own : r.total;  // query c's key limit
+  const int lim_c = (int)(own < r.total ? own : r.total);  // query c's key limit (keys fit in 32 bits)
   auto load_k = [&](KVTile<D>& t, int64_t k) {
     const int64_t kb = (sp + k * r.nact) * 32;  // < total <= cache_len
     const int64_t kmax = last_key - kb, vstop = r.total - kb;
@@ -377,7 +455,7 @@ __global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(Attn
                          vstop < 32 ? (int)vstop : 32, c, g);
   };
   auto attend_k = [&](const KVTile<D>& t, int64_t k) {
-    attend<D>(t, qop, c_scale, st, o, g, (sp + k * r.nact) * 32 + 8 * g, lim_c);
+    attend<D>(t, qop, c_scale, st, o, g, (int)((sp + k * r.nact) * 32) + 8 * g, lim_c);
   };
   if (ntot > 0) {
     KVTile<D> A;
@@ -405,6 +483,22 @@ __global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(Attn
       }
     }
   }
+
+}
+
+// Split-K: one wave per (split, head, row); the split's partial (or, for a row with one split, the output) goes to
+// HBM and a second launch (or the row's last split) merges them.
+template <int D, bool PIPE>
+__global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(AttnArgs a) {
+  constexpr int NG = D / 128;
+  const int sp = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const SplitRange r = split_range(a, b, sp);
+  if (sp >= r.nact) return;
+  const int lane = threadIdx.x, c = lane & 15, g = lane >> 4;
+  const int T = a.T;
+  SoftmaxState st;
+  f32x4_t o[NG * 8];
+  attend_split<D, PIPE>(a, b, h, sp, r, st, o);
 
   // ---- finish: per-query sums, then either the output or this split's partial
   float l_tot = st.l_run + __shfl_xor(st.l_run, 16, kWave);
@@ -454,6 +548,68 @@ __global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(Attn
     put_partial(a.part_ml + (base + c) * 2 + 1, l_tot, through);
   }
   finish_split<uint16_t>(a, b, h, r.nact);
+}
+
+// ---------------------------------------------------------------------------------------------- workgroup per row
+
+constexpr int kWgWaves = 8;
+constexpr int kWgMaxT = 15;  // the waves' partials stay within 64 KB of LDS
+constexpr int64_t kWgMinUnits = 128;  // rows x heads from which one workgroup per (head, row) beats split-K
+
+// kWgWaves waves per (head, row), wave w taking tiles w, w + 8, w + 16, ... of the row; their partials meet in LDS
+// and the workgroup writes the output: no partials in HBM and no second launch.  One such workgroup fills a CU
+// (two waves per SIMD), so the launcher uses it when rows x heads cover the CUs.
+template <int D>
+__global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_wg_kernel(AttnArgs a) {
+  constexpr int NG = D / 128;
+  extern __shared__ float smem[];  // [waves][T][D] partial outputs, [waves][T] m, [waves][T] l
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const int T = a.T, Dn = a.D;
+  SplitRange r = split_range(a, b, 0);
+  r.nact = kWgWaves;
+  SoftmaxState st;
+  f32x4_t o[NG * 8];
+  attend_split<D, true>(a, b, h, w, r, st, o);
+  float l_tot = st.l_run + __shfl_xor(st.l_run, 16, kWave);
+  l_tot += __shfl_xor(l_tot, 32, kWave);
+  float* po = smem;
+  float* pm = smem + kWgWaves * T * D;
+  float* pl = pm + kWgWaves * T;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = 4 * g + i;
+    if (t >= T) continue;
+#pragma unroll
+    for (int gg = 0; gg < NG; ++gg) {
+      f32x4_t* dst = reinterpret_cast<f32x4_t*>(po + (w * T + t) * D + gg * 128 + c * 8);
+      dst[0] = f32x4_t{o[gg * 8 + 0][i], o[gg * 8 + 1][i], o[gg * 8 + 2][i], o[gg * 8 + 3][i]};
+      dst[1] = f32x4_t{o[gg * 8 + 4][i], o[gg * 8 + 5][i], o[gg * 8 + 6][i], o[gg * 8 + 7][i]};
+    }
+  }
+  if (g == 0 && c < T) {
+    pm[w * T + c] = st.m_ref;
+    pl[w * T + c] = l_tot;
+  }
+  __syncthreads();
+  uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
+  for (int idx = threadIdx.x; idx < T * (D / 4); idx += 64 * kWgWaves) {
+    const int t = idx / (D / 4), d = (idx - t * (D / 4)) * 4;
+    float top = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < kWgWaves; ++v) top = fmaxf(top, pm[v * T + t]);
+    float den = 0.f;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < kWgWaves; ++v) {
+      const float m = pm[v * T + t];
+      const float wt = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - top);
+      den += wt * pl[v * T + t];
+      acc += wt * *reinterpret_cast<const f32x4_t*>(po + (v * T + t) * D + d);
+    }
+    const float div = den > 0.f ? den : 1.f;
+    store4<uint16_t>(out + ((int64_t)(b * T + t) * a.H + h) * Dn + d, acc / div);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------- VALU
@@ -666,8 +822,7 @@ extern "C" size_t omni_verify_attention_workspace(int32_t rows, int32_t tokens, 
                                                   int32_t head_dim, int32_t keys, int32_t chunk) {
   if (rows <= 0 || tokens <= 0 || heads <= 0 || head_dim <= 0 || keys <= 0) return 0;
   if (chunk <= 0) chunk = omni_verify_attention_chunk(rows, tokens, heads, head_dim, keys);
-  const size_t splits = (size_t)attn_splits(keys, chunk);
-  const size_t units = (size_t)rows * heads * splits * tokens;
+  const size_t units = (size_t)rows * heads * attn_splits(keys, chunk) * tokens;
   return align256(units * head_dim * sizeof(float)) + align256(units * 2 * sizeof(float));
 }
 
@@ -774,6 +929,16 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
   a.ctx_splits = splits;
   a.gen_split = -1;
   hipStream_t s = (hipStream_t)stream;
+  const bool wg = dtype == OMNI_BF16 && head_dim == 128 && stride_pos == head_dim && tokens <= kWgMaxT &&
+                  !(flags & OMNI_ATTN_SPLIT_K) && (int64_t)rows * heads >= kWgMinUnits;
+  if (wg) {  // one workgroup per (head, row): the whole key range is one split of kWgWaves waves
+    a.chunk = (keys + 31) / 32 * 32;
+    a.ctx_splits = 1;
+    a.splits = 1;
+    const size_t lds = (size_t)kWgWaves * tokens * (head_dim + 2) * sizeof(float);
+    verify_attn_wg_kernel<128><<<dim3(heads, rows), 64 * kWgWaves, lds, s>>>(a);
+    return omni_launch_status();
+  }
   st = launch_attention(a, rows, dtype, s);
   if (st != OMNI_OK || !a.separate) return st;
   return launch_combine(a, rows, dtype, s);

@@ -29,12 +29,13 @@ import torch
 
 from . import _lib
 
-# Launch settings of draft_attention / decode_attention: ``chunk`` keys per split (0: the library's
-# choice for the launch shape), ``separate``: merge the splits in a second launch (else the last
-# split of each row and head merges them after agent-scope fences -- an L2 write-back per wave on
-# gfx950, measured several times slower than the second launch).
-DRAFT_ATTN = {"chunk": 0, "separate": True}
-ATTN = {"chunk": 0, "separate": True}
+# Launch settings of draft_attention / decode_attention.  ``split_k``: always split the keys over waves of their
+# own (otherwise the library runs one 8-wave workgroup per (head, row) when rows x heads cover the CUs, merging in
+# LDS).  Split-K only: ``chunk`` keys per split (0: the library's choice for the launch shape), ``separate``: merge
+# the splits in a second launch (else the last split of each row and head merges them, reading the other splits'
+# partials through to the coherence point -- measured slower than the second launch).
+DRAFT_ATTN = {"chunk": 0, "separate": True, "split_k": False}
+ATTN = {"chunk": 0, "separate": True, "split_k": False}
 
 _counters: dict[int, torch.Tensor] = {}
 # Ticket buffers replaced by larger ones: captured graphs may still hold their addresses, so they
@@ -123,7 +124,7 @@ def _attn_counters(device: torch.device, n: int) -> torch.Tensor:
 
 
 def _verify(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor, tokens: int,
-            keys: int, scale: float, chunk: int, separate: bool) -> torch.Tensor:
+            keys: int, scale: float, chunk: int, separate: bool, split_k: bool = False) -> torch.Tensor:
     lib = _lib.load()
     rows_total, heads, dim = q.shape
     _need(rows_total % tokens == 0, "q: [B*T, H, D]")
@@ -140,7 +141,7 @@ def _verify(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengt
     workspace = torch.empty(max(ws, 256), device=q.device, dtype=torch.uint8)
     counters = _attn_counters(q.device, groups * heads)
     out = torch.empty_like(q)
-    flags = _lib.ATTN_SEPARATE_COMBINE if separate else 0
+    flags = (_lib.ATTN_SEPARATE_COMBINE if separate else 0) | (_lib.ATTN_SPLIT_K if split_k else 0)
     status = lib.omni_verify_attention(
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
         k_cache.stride(2), k_cache.size(2), lengths.data_ptr(), groups, tokens, heads, dim, keys, chunk,
@@ -158,7 +159,7 @@ def draft_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     ``DRAFT_ATTN`` (the reference's Triton settings -- block, warps, stages, programs -- have no meaning here and
     are ignored).  (src/omniasr_trt/kernels.py:338-358)"""
     cfg = {**DRAFT_ATTN, **{k: v for k, v in launch.items() if k in DRAFT_ATTN}}
-    return _verify(q, k_cache, v_cache, lengths, tokens, keys, scale, cfg["chunk"], cfg["separate"])
+    return _verify(q, k_cache, v_cache, lengths, tokens, keys, scale, cfg["chunk"], cfg["separate"], cfg["split_k"])
 
 
 def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor,
@@ -170,7 +171,7 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     (src/omniasr_trt/kernels.py:406-423)"""
     del block, warps, stages, programs
     return _verify(q, k_cache, v_cache, lengths, 1, keys, scale, ATTN["chunk"] if chunk is None else chunk,
-                   ATTN["separate"])
+                   ATTN["separate"], ATTN["split_k"])
 
 
 def beam_attention(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, ctx_len: torch.Tensor, kg: torch.Tensor,

@@ -133,6 +133,17 @@ def test_verify_attention_config3(cuda, t):
     _attn_case(cuda, torch.bfloat16, 8, 32, 128, t, keys, lengths, keys, 1003, BF16_TOL)
 
 
+@pytest.mark.parametrize("t", [1, 5, 9, 15, 16])
+def test_verify_attention_workgroup_and_split_k(cuda, t):
+    """8 rows x 32 heads: one 8-wave workgroup per (head, row) (T <= 15) and split-K on the same inputs, both
+    against the oracle; rows shorter than one tile per wave, empty, and ending inside a tile."""
+    lengths = torch.tensor([2400, 0, 31, 257, 1023, 7, 1800, 96])
+    keys = -(-(int(lengths.max()) + t) // 256) * 256
+    a = _attn_case(cuda, torch.bfloat16, 8, 32, 128, t, keys, lengths, keys, 31 + t, BF16_TOL)
+    b = _attn_case(cuda, torch.bfloat16, 8, 32, 128, t, keys, lengths, keys, 31 + t, BF16_TOL, split_k=True)
+    torch.testing.assert_close(a.float(), b.float(), atol=1e-2, rtol=1e-2)
+
+
 def test_verify_attention_split_choices_agree(cuda):
     """Every split size and both merge modes give the oracle's result, and the two merge modes agree."""
     lengths = torch.tensor([1500, 3, 700, 64, 0, 1023])
@@ -153,23 +164,24 @@ def test_verify_attention_tickets_left_zero(cuda):
     assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
 
 
-def test_verify_attention_graph_replays(cuda):
-    """Captured in a HIP graph: every replay equals the eager result bit for bit."""
+@pytest.mark.parametrize("split_k", [False, True])
+def test_verify_attention_graph_replays(cuda, split_k):
+    """Captured in a HIP graph: every replay equals the eager result bit for bit (both decompositions)."""
     g = gen(8)
     b, h, d, t, cap = 8, 32, 128, 5, 2560
     kc = torch.randn(b, h, cap, d, generator=g).to(torch.bfloat16).to(cuda)
     vc = torch.randn(b, h, cap, d, generator=g).to(torch.bfloat16).to(cuda)
     q = torch.randn(b * t, h, d, generator=g).to(torch.bfloat16).to(cuda)
     lengths = torch.randint(750, 2401, (b,), generator=g).to(cuda)
-    eager = kernels.draft_attention(q, kc, vc, lengths, t, cap, d ** -0.5)
+    eager = kernels.draft_attention(q, kc, vc, lengths, t, cap, d ** -0.5, split_k=split_k)
     torch.cuda.synchronize()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(s):
-        kernels.draft_attention(q, kc, vc, lengths, t, cap, d ** -0.5)
+        kernels.draft_attention(q, kc, vc, lengths, t, cap, d ** -0.5, split_k=split_k)
         graph.capture_begin()
-        out = kernels.draft_attention(q, kc, vc, lengths, t, cap, d ** -0.5)
+        out = kernels.draft_attention(q, kc, vc, lengths, t, cap, d ** -0.5, split_k=split_k)
         graph.capture_end()
     torch.cuda.current_stream().wait_stream(s)
     for i in range(4):
@@ -179,7 +191,7 @@ def test_verify_attention_graph_replays(cuda):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), i
-        kernels.draft_attention(q, kc, vc, lengths, t, cap, d ** -0.5)  # eager work between replays
+        kernels.draft_attention(q, kc, vc, lengths, t, cap, d ** -0.5, split_k=split_k)  # eager work between replays
         torch.cuda.synchronize()
 
 
