@@ -538,7 +538,7 @@ def main() -> int:
                    "generated_per_slot": GENERATE, "drafter": "own tokens (ngram 8, self_min 3: the reference's)",
                    "repetition_stop": "off (EOS suppressed; slots stop at their budget)", "sync_every": 8,
                    "tokens_per_row_step": round(tokens / max(row_steps, 1), 3), "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "hbm", "kernel": "verify_attn_wg_kernel<128> (config 3, T = 5)",
+        "roofline": {"bound": "hbm", "kernel": "verify_attn_pair_kernel<128> (config 3, T = 5)",
                      "achieved": attn["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": attn["frac_peak"],
                      "traffic": measured_traffic(), "bytes_per_launch": attn["bytes"], "us_per_launch": attn["us"]},
         "cpu_baseline": cpu,

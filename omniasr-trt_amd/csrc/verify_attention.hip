@@ -401,7 +401,8 @@ __device__ __forceinline__ void attend(const KVTile<D>& t, const u32x4_t (&qop)[
 // PIPE: two tiles of registers, the next tile's loads in flight during the current tile's math.
 template <int D, bool PIPE>
 __device__ __forceinline__ void attend_split(const AttnArgs& a, int b, int h, int sp, const SplitRange& r,
-                                             SoftmaxState& st, f32x4_t (&o)[D / 16]) {
+                                             SoftmaxState& st, f32x4_t (&o)[D / 16], int64_t t0 = 0,
+                                             int64_t t1 = -1) {
   constexpr int KS = D / 32;  // k-steps of S^T = K Q^T
   constexpr int NG = D / 128;  // 128-wide output groups
   const int lane = lane_id(), c = lane & 15, g = lane >> 4;
@@ -426,36 +427,31 @@ __device__ __forceinline__ void attend_split(const AttnArgs& a, int b, int h, in
 #pragma unroll
   for (int nb = 0; nb < NG * 8; ++nb) o[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};  // row 4g + i, dimension 128gg + 8c + e
 
-  // The row's 32-key tiles are dealt out round-robin over its nact splits: split sp takes tiles sp, sp + nact,
-  // sp + 2 nact, ...  Each split gets the same number of tiles (give or take one), and at any moment the row's
-  // splits read neighbouring tiles (DRAM locality), unlike contiguous per-split ranges.  Tiles below
-  // min(total, n) are seen whole by every query: no masks, no clamps.
+  // The row's 32-key tiles t0, t0 + 1, ... < t1 (default: all of them) are dealt out round-robin over the nact
+  // splits: split sp takes tiles t0 + sp, t0 + sp + nact, ...  Each split gets the same number of tiles (give or
+  // take one), and at any moment the splits read neighbouring tiles (DRAM locality), unlike contiguous ranges.
+  // One branch-free loader and one attend routine serve whole tiles and those reaching past some query's last
+  // key, so the only branches around the loads are the loop's own: the wait before a tile's math then leaves the
+  // next tile's loads in flight (a load under a condition makes the compiler wait for every outstanding load
+  // where the branches join).
   const int64_t row_tiles = (r.total + 31) >> 5;
-  const int64_t see_all = r.total < r.n ? r.total : r.n;
-  const int64_t full_tiles = see_all >> 5;  // tiles [0, full_tiles) are full
-  const int64_t nfull = full_tiles > sp ? (full_tiles - sp + r.nact - 1) / r.nact : 0;
+  const int64_t end = t1 < 0 || t1 > row_tiles ? row_tiles : t1;
+  const int64_t first = t0 + sp;
+  const int64_t ntot = first < end ? (end - first + r.nact - 1) / r.nact : 0;
   // The launcher sends only caches with contiguous key rows (s_pos == D) here.
-  const char* kt = reinterpret_cast<const char*>(kbase) + (int64_t)sp * 32 * a.s_pos * 2;
-  const char* vt = reinterpret_cast<const char*>(vbase) + (int64_t)sp * 32 * a.s_pos * 2;
+  const char* kt = reinterpret_cast<const char*>(kbase) + first * 32 * a.s_pos * 2;
+  const char* vt = reinterpret_cast<const char*>(vbase) + first * 32 * a.s_pos * 2;
   const int64_t tile_bytes = (int64_t)r.nact * 32 * a.s_pos * 2;  // stride between this split's tiles
-
-  // The split's tiles in order: nfull tiles every query sees whole, then at most two reaching past some query's
-  // last key.  One branch-free loader and one attend routine serve both kinds, so the only branches around the
-  // loads are the loop's own: the wait before a tile's math then leaves the next tile's loads in flight (a load
-  // under a condition makes the compiler wait for every outstanding load where the branches join).
-  const int64_t ntail =
-      row_tiles > sp + nfull * r.nact ? (row_tiles - sp - nfull * r.nact + r.nact - 1) / r.nact : 0;
-  const int64_t ntot = nfull + ntail;
   const int64_t own = r.n + (a.causal ? c : 0);
   const int lim_c = (int)(own < r.total ? own : r.total);  // query c's key limit (keys fit in 32 bits)
   auto load_k = [&](KVTile<D>& t, int64_t k) {
-    const int64_t kb = (sp + k * r.nact) * 32;  // < total <= cache_len
+    const int64_t kb = (first + k * r.nact) * 32;  // < total <= cache_len
     const int64_t kmax = last_key - kb, vstop = r.total - kb;
     load_tile_clamped<D>(t, kt + k * tile_bytes, vt + k * tile_bytes, kmax < 31 ? (int)kmax : 31,
                          vstop < 32 ? (int)vstop : 32, c, g);
   };
   auto attend_k = [&](const KVTile<D>& t, int64_t k) {
-    attend<D>(t, qop, c_scale, st, o, g, (int)((sp + k * r.nact) * 32) + 8 * g, lim_c);
+    attend<D>(t, qop, c_scale, st, o, g, (int)((first + k * r.nact) * 32) + 8 * g, lim_c);
   };
   if (ntot > 0) {
     KVTile<D> A;
@@ -553,62 +549,140 @@ __global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(Attn
 // ---------------------------------------------------------------------------------------------- workgroup per row
 
 constexpr int kWgWaves = 8;
-constexpr int kWgMaxT = 15;  // the waves' partials stay within 64 KB of LDS
+constexpr int kWgMaxT = 14;  // the waves' partials and the row ranking stay within 64 KB of LDS
 constexpr int64_t kWgMinUnits = 128;  // rows x heads from which one workgroup per (head, row) beats split-K
 
-// kWgWaves waves per (head, row), wave w taking tiles w, w + 8, w + 16, ... of the row; their partials meet in LDS
-// and the workgroup writes the output: no partials in HBM and no second launch.  One such workgroup fills a CU
-// (two waves per SIMD), so the launcher uses it when rows x heads cover the CUs.
+constexpr int kPairMaxRows = 256;
+
+// The row's tile count: 32-key tiles up to the keys its last query sees.
+__device__ __forceinline__ int row_tile_count(const AttnArgs& a, int b) {
+  const SplitRange r = split_range(a, b, 0);
+  return (int)((r.total + 31) >> 5);
+}
+
+// One 8-wave workgroup per (head, row) unit, but working on halves: units are ranked by length, and workgroup i
+// takes the first half of the i-th longest unit and the second half of the i-th shortest, so the workgroups (one
+// per CU) stream about the same number of tiles.  That balance is what the HBM needs: a CU reads at most ~30 GB/s,
+// so the GPU streams at full rate only while nearly every CU is busy.  In each half the 8 waves take interleaved
+// tiles and merge in LDS; the half's partial is written through to the coherence point, and the second of a
+// unit's two halves to finish merges them (one round of loads) and writes the output.
 template <int D>
-__global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_wg_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(AttnArgs a, int rows, int slots) {
   constexpr int NG = D / 128;
   extern __shared__ float smem[];  // [waves][T][D] partial outputs, [waves][T] m, [waves][T] l
-  const int h = blockIdx.x, b = blockIdx.y;
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-  const int T = a.T, Dn = a.D;
-  SplitRange r = split_range(a, b, 0);
-  r.nact = kWgWaves;
-  SoftmaxState st;
-  f32x4_t o[NG * 8];
-  attend_split<D, true>(a, b, h, w, r, st, o);
-  float l_tot = st.l_run + __shfl_xor(st.l_run, 16, kWave);
-  l_tot += __shfl_xor(l_tot, 32, kWave);
+  __shared__ int ntl[kPairMaxRows];
+  __shared__ int order[kPairMaxRows];  // rows by tile count, longest first (ties: lower row first)
+  __shared__ int s_tickets[2];
+  const int tid = threadIdx.x, lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int T = a.T, H = a.H, U = rows * H;
+  for (int b = tid; b < rows; b += 64 * kWgWaves) ntl[b] = row_tile_count(a, b);
+  __syncthreads();
+  for (int b = tid; b < rows; b += 64 * kWgWaves) {
+    const int nb = ntl[b];
+    int rank = 0;
+    for (int b2 = 0; b2 < rows; ++b2) rank += (ntl[b2] > nb) || (ntl[b2] == nb && b2 < b);
+    order[rank] = b;
+  }
+  __syncthreads();
+  const int i = blockIdx.x;
+  int unit[2];
+  unit[0] = order[i / H] * H + i % H;                      // the i-th longest unit: its first half
+  unit[1] = order[(U - 1 - i) / H] * H + (U - 1 - i) % H;  // the i-th shortest: its second half
   float* po = smem;
   float* pm = smem + kWgWaves * T * D;
   float* pl = pm + kWgWaves * T;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = 4 * g + i;
-    if (t >= T) continue;
-#pragma unroll
-    for (int gg = 0; gg < NG; ++gg) {
-      f32x4_t* dst = reinterpret_cast<f32x4_t*>(po + (w * T + t) * D + gg * 128 + c * 8);
-      dst[0] = f32x4_t{o[gg * 8 + 0][i], o[gg * 8 + 1][i], o[gg * 8 + 2][i], o[gg * 8 + 3][i]};
-      dst[1] = f32x4_t{o[gg * 8 + 4][i], o[gg * 8 + 5][i], o[gg * 8 + 6][i], o[gg * 8 + 7][i]};
-    }
-  }
-  if (g == 0 && c < T) {
-    pm[w * T + c] = st.m_ref;
-    pl[w * T + c] = l_tot;
-  }
-  __syncthreads();
   uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
-  for (int idx = threadIdx.x; idx < T * (D / 4); idx += 64 * kWgWaves) {
-    const int t = idx / (D / 4), d = (idx - t * (D / 4)) * 4;
-    float top = -INFINITY;
 #pragma unroll
-    for (int v = 0; v < kWgWaves; ++v) top = fmaxf(top, pm[v * T + t]);
-    float den = 0.f;
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int half = 0; half < 2; ++half) {
+    const int u = unit[half], b = u / H, h = u - b * H;
+    SplitRange r = split_range(a, b, 0);
+    r.nact = kWgWaves;
+    const int64_t nt = (r.total + 31) >> 5, hm = (nt + 1) >> 1;
+    SoftmaxState st;
+    f32x4_t o[NG * 8];
+    attend_split<D, true>(a, b, h, w, r, st, o, half == 0 ? 0 : hm, half == 0 ? hm : nt);
+    float l_tot = st.l_run + __shfl_xor(st.l_run, 16, kWave);
+    l_tot += __shfl_xor(l_tot, 32, kWave);
 #pragma unroll
-    for (int v = 0; v < kWgWaves; ++v) {
-      const float m = pm[v * T + t];
-      const float wt = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - top);
-      den += wt * pl[v * T + t];
-      acc += wt * *reinterpret_cast<const f32x4_t*>(po + (v * T + t) * D + d);
+    for (int ii = 0; ii < 4; ++ii) {
+      const int t = 4 * g + ii;
+      if (t >= T) continue;
+#pragma unroll
+      for (int gg = 0; gg < NG; ++gg) {
+        f32x4_t* dst = reinterpret_cast<f32x4_t*>(po + (w * T + t) * D + gg * 128 + c * 8);
+        dst[0] = f32x4_t{o[gg * 8 + 0][ii], o[gg * 8 + 1][ii], o[gg * 8 + 2][ii], o[gg * 8 + 3][ii]};
+        dst[1] = f32x4_t{o[gg * 8 + 4][ii], o[gg * 8 + 5][ii], o[gg * 8 + 6][ii], o[gg * 8 + 7][ii]};
+      }
     }
-    const float div = den > 0.f ? den : 1.f;
-    store4<uint16_t>(out + ((int64_t)(b * T + t) * a.H + h) * Dn + d, acc / div);
+    if (g == 0 && c < T) {
+      pm[w * T + c] = st.m_ref;
+      pl[w * T + c] = l_tot;
+    }
+    __syncthreads();
+    float* gpo = a.part_o + ((int64_t)u * slots + half) * T * D;
+    float* gml = a.part_ml + ((int64_t)u * slots + half) * T * 2;
+    for (int idx = tid; idx < T * (D / 4); idx += 64 * kWgWaves) {
+      const int t = idx / (D / 4), d = (idx - t * (D / 4)) * 4;
+      float top = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < kWgWaves; ++v) top = fmaxf(top, pm[v * T + t]);
+      float den = 0.f;
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int v = 0; v < kWgWaves; ++v) {
+        const float mv = pm[v * T + t];
+        const float wt = mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - top);
+        den += wt * pl[v * T + t];
+        acc += wt * *reinterpret_cast<const f32x4_t*>(po + (v * T + t) * D + d);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) put_partial(gpo + t * D + d + e, acc[e], true);
+      if (d == 0) {
+        put_partial(gml + t * 2, top, true);
+        put_partial(gml + t * 2 + 1, den, true);
+      }
+    }
+    __syncthreads();  // the LDS partials are rewritten by the next half
+  }
+  // Both halves' partials have reached the coherence point: take the units' tickets; the second half of a unit
+  // to arrive merges the two.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (tid < 2) s_tickets[tid] = __hip_atomic_fetch_add(&a.counters[unit[tid]], 1, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  for (int q = 0; q < 2; ++q) {
+    if (s_tickets[q] != 1) continue;  // uniform over the workgroup
+    const int u = unit[q], b = u / H, h = u - b * H;
+    for (int idx = tid; idx < T * (D / 4); idx += 64 * kWgWaves) {
+      const int t = idx / (D / 4), d = (idx - t * (D / 4)) * 4;
+      float mv[2], lv[2];
+      f32x4_t ov[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float* ml = a.part_ml + (((int64_t)u * slots + e) * T + t) * 2;
+        const uint64_t mlv = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(ml)), __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+        mv[e] = __uint_as_float((uint32_t)mlv);
+        lv[e] = __uint_as_float((uint32_t)(mlv >> 32));
+        ov[e] = get_through4(a.part_o + (((int64_t)u * slots + e) * T + t) * D + d);
+      }
+      const float top = fmaxf(mv[0], mv[1]);
+      float den = 0.f;
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float wt = mv[e] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv[e] - top);
+        den += wt * lv[e];
+        acc += wt * ov[e];
+      }
+      const float div = den > 0.f ? den : 1.f;
+      store4<uint16_t>(out + ((int64_t)(b * T + t) * H + h) * D + d, acc / div);
+    }
+    if (tid == 0) __hip_atomic_store(&a.counters[u], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -818,11 +892,17 @@ extern "C" int32_t omni_verify_attention_chunk(int32_t rows, int32_t tokens, int
 
 static size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
+// Partial slots per unit in the workspace: split-K at this chunk, or stream-K.
+static size_t attn_slots(int keys, int chunk) {
+  const int splits = attn_splits(keys, chunk);
+  return (size_t)(splits > 2 ? splits : 2);  // split-K's splits, or a unit's two halves
+}
+
 extern "C" size_t omni_verify_attention_workspace(int32_t rows, int32_t tokens, int32_t heads,
                                                   int32_t head_dim, int32_t keys, int32_t chunk) {
   if (rows <= 0 || tokens <= 0 || heads <= 0 || head_dim <= 0 || keys <= 0) return 0;
   if (chunk <= 0) chunk = omni_verify_attention_chunk(rows, tokens, heads, head_dim, keys);
-  const size_t units = (size_t)rows * heads * attn_splits(keys, chunk) * tokens;
+  const size_t units = (size_t)rows * heads * attn_slots(keys, chunk) * tokens;
   return align256(units * head_dim * sizeof(float)) + align256(units * 2 * sizeof(float));
 }
 
@@ -904,7 +984,7 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
   if (!attention_aligned(q, out, k_cache, v_cache, stride_row, stride_head, stride_pos, head_dim, dtype))
     return OMNI_ERR_INVALID;
   const int splits = attn_splits(keys, chunk);
-  const size_t units = (size_t)rows * heads * splits * tokens;
+  const size_t units = (size_t)rows * heads * attn_slots(keys, chunk) * tokens;
   AttnArgs a;
   a.q = q;
   a.k = k_cache;
@@ -930,13 +1010,14 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
   a.gen_split = -1;
   hipStream_t s = (hipStream_t)stream;
   const bool wg = dtype == OMNI_BF16 && head_dim == 128 && stride_pos == head_dim && tokens <= kWgMaxT &&
-                  !(flags & OMNI_ATTN_SPLIT_K) && (int64_t)rows * heads >= kWgMinUnits;
+                  rows <= kPairMaxRows && !(flags & OMNI_ATTN_SPLIT_K) && (int64_t)rows * heads >= kWgMinUnits;
   if (wg) {  // one workgroup per (head, row): the whole key range is one split of kWgWaves waves
     a.chunk = (keys + 31) / 32 * 32;
     a.ctx_splits = 1;
     a.splits = 1;
+    const int slots = (int)attn_slots(keys, chunk);
     const size_t lds = (size_t)kWgWaves * tokens * (head_dim + 2) * sizeof(float);
-    verify_attn_wg_kernel<128><<<dim3(heads, rows), 64 * kWgWaves, lds, s>>>(a);
+    verify_attn_pair_kernel<128><<<rows * heads, 64 * kWgWaves, lds, s>>>(a, rows, slots);
     return omni_launch_status();
   }
   st = launch_attention(a, rows, dtype, s);

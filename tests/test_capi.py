@@ -41,7 +41,8 @@ def test_workspace_and_split_queries():
         chunk = lib.omni_verify_attention_chunk(rows, t, h, d, keys)
         assert chunk % 32 == 0 and 32 <= chunk <= max(64, -(-keys // 32) * 32)
         splits = -(-keys // chunk)
-        units = rows * h * splits * t
+        slots = max(splits, 2)  # split-K partials, or a unit's two halves
+        units = rows * h * slots * t
         want = -(-units * d * 4 // 256) * 256 + -(-units * 2 * 4 // 256) * 256
         assert lib.omni_verify_attention_workspace(rows, t, h, d, keys, 0) == want
     # config 3: 8 rows x 32 heads, keys 2560 -> 320 keys for 2048 waves, capped at 8 tiles per split
