@@ -100,6 +100,18 @@ __device__ __forceinline__ void put_partial(float* p, float v, bool through) {
   else *p = v;
 }
 
+// Four floats written through to the coherence point in one 16-byte store (agent scope: the cache-policy bit the
+// compiler sets on agent-scope atomic stores).  Only waited for by an explicit s_waitcnt.
+__device__ __forceinline__ void put_through4(float* p, f32x4_t v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+
+// Two floats (m, l) written through in one 8-byte agent-scope store.
+__device__ __forceinline__ void put_through2(float* p, float x, float y) {
+  const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ float get_through(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -636,12 +648,8 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
         den += wt * pl[v * T + t];
         acc += wt * *reinterpret_cast<const f32x4_t*>(po + (v * T + t) * D + d);
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) put_partial(gpo + t * D + d + e, acc[e], true);
-      if (d == 0) {
-        put_partial(gml + t * 2, top, true);
-        put_partial(gml + t * 2 + 1, den, true);
-      }
+      put_through4(gpo + t * D + d, acc);
+      if (d == 0) put_through2(gml + t * 2, top, den);
     }
     __syncthreads();  // the LDS partials are rewritten by the next half
   }
