@@ -126,9 +126,11 @@ size_t omni_beam_attention_workspace(int32_t groups, int32_t beams, int32_t head
  * generated keys j < gen_len[r], key j read at row ptr[r*ptr_stride + j] of ``k_gen`` / ``v_gen``
  * (strides gen_row / gen_head / gen_pos, ``gen_rows`` rows of ``gen_cap`` positions); pointers are
  * clamped into [0, gen_rows).  out = softmax(q.k * scale) . v over both parts, fp32 accumulation; no
- * key at all gives zeros.  One pass over a group's context serves all of its beams (the MFMA kernel
- * of omni_verify_attention with every query over the same keys); the generated keys are read by a
- * pointer-chasing kernel into one more partial; a merge launch combines them.
+ * key at all gives zeros.  One pass over a group's context serves all of its beams (the kernels of
+ * omni_verify_attention with every query over the same keys); the generated keys are read by a
+ * pointer-chasing kernel into one more partial.  bf16, head_dim 128, contiguous key rows, beams <= 14 and
+ * groups * heads >= 128: the context halves kernel merges that partial in its last step (``counters``:
+ * groups*heads int32 tickets, zero before the first call, left zero); otherwise split-K and a merge launch.
  * ``chunk``: context keys per split (0: the library's choice).  ``workspace``: at least
  * omni_beam_attention_workspace() bytes, 256-byte aligned.  beams: 1..16.
  */
@@ -138,8 +140,8 @@ int omni_beam_attention(const void *q, const void *k_ctx, const void *v_ctx, int
                         int64_t gen_pos, int64_t gen_cap, int64_t gen_rows, const int32_t *ptr,
                         int64_t ptr_stride, const int64_t *gen_len, int32_t groups, int32_t beams,
                         int32_t heads, int32_t head_dim, int32_t ctx_keys, int32_t chunk, float scale,
-                        void *out, void *workspace, size_t workspace_bytes, int32_t dtype,
-                        void *stream);
+                        void *out, void *workspace, size_t workspace_bytes, int32_t *counters,
+                        int32_t dtype, void *stream);
 
 /*
  * Draft proposal of every row.  Replaces ``kernels.propose`` / ``_propose``

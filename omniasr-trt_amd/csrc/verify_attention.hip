@@ -7,13 +7,19 @@
 // log-sum-exp with w_s = exp(m_s - max m) (0 for an empty split) and out = sum w_s acc_s /
 // sum w_s l_s (0 when that sum is 0).
 //
-// Work decomposition: one wavefront per (key split, head, row) -- grid (splits, heads, rows), 64
-// threads.  A wave streams its split's keys 32 at a time and serves all of the row's T <= 16
-// queries with that single read of K and V.  Splits beyond a row's last key exit at once, so the
-// grid depends on the key bucket only (graph capture) while ragged rows read just their own keys.
-// The last split of a (row, head) to finish merges the partials (an atomic ticket per (row, head),
-// reset by the merging wave); a row with one split writes its output directly.
-//
+// Work decompositions.  The unit of work is a (head, row) pair; one wave serves all of the row's T <= 16 queries
+// with a single read of K and V, 32 keys at a time.
+//  * Halves (bf16, head_dim 128, T <= 14, rows x heads >= 128; verify_attn_pair_kernel): one 8-wave workgroup
+//    per CU-sized share, each taking the first half of a long unit and the second half of a short one (units
+//    ranked by length on the device), so every CU streams about the same number of tiles -- a CU reads at most
+//    ~30 GB/s, so HBM runs at full rate only while nearly all CUs are busy.  The 8 waves interleave a half's tiles
+//    and merge in LDS; the second half of a unit to finish merges the two halves (partials written through to the
+//    coherence point, atomic ticket per unit).  One launch, no partials in HBM beyond 2 x T x D per unit.
+//  * Split-K (every other shape; verify_attn_mfma_kernel / verify_attn_valu_kernel): one wavefront per (key
+//    split, head, row), grid (splits, heads, rows).  A row's 32-key tiles are dealt round-robin over its splits.
+//    Splits beyond a row's last key exit at once, so the grid depends on the key bucket only (graph capture)
+//    while ragged rows read just their own keys.  The splits' partials are merged by a second launch or by the
+//    last split to finish (ticket per (row, head)); a row with one split writes its output directly.
 // bf16, head_dim a multiple of 128: both products run on v_mfma_f32_16x16x32_bf16 with the T
 // queries padded to the 16-wide MFMA dimension, and every K/V element is loaded straight into the
 // MFMA operand layout with 128-bit loads (no LDS):
@@ -662,27 +668,35 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
   if (tid < 2) s_tickets[tid] = __hip_atomic_fetch_add(&a.counters[unit[tid]], 1, __ATOMIC_RELAXED,
                                                        __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
+  // Beams: a third partial, the generated keys', written by the previous launch at slot gen_split.
+  const int nparts = a.gen_split >= 0 ? 3 : 2;
   for (int q = 0; q < 2; ++q) {
     if (s_tickets[q] != 1) continue;  // uniform over the workgroup
     const int u = unit[q], b = u / H, h = u - b * H;
     for (int idx = tid; idx < T * (D / 4); idx += 64 * kWgWaves) {
       const int t = idx / (D / 4), d = (idx - t * (D / 4)) * 4;
-      float mv[2], lv[2];
-      f32x4_t ov[2];
+      float mv[3], lv[3];
+      f32x4_t ov[3];
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const float* ml = a.part_ml + (((int64_t)u * slots + e) * T + t) * 2;
-        const uint64_t mlv = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(ml)), __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-        mv[e] = __uint_as_float((uint32_t)mlv);
-        lv[e] = __uint_as_float((uint32_t)(mlv >> 32));
-        ov[e] = get_through4(a.part_o + (((int64_t)u * slots + e) * T + t) * D + d);
+      for (int e = 0; e < 3; ++e) {
+        mv[e] = -INFINITY;
+        lv[e] = 0.f;
+        ov[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if (e < nparts) {
+          const int slot = e < 2 ? e : a.gen_split;
+          const float* ml = a.part_ml + (((int64_t)u * slots + slot) * T + t) * 2;
+          const uint64_t mlv = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(ml)),
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          mv[e] = __uint_as_float((uint32_t)mlv);
+          lv[e] = __uint_as_float((uint32_t)(mlv >> 32));
+          ov[e] = get_through4(a.part_o + (((int64_t)u * slots + slot) * T + t) * D + d);
+        }
       }
-      const float top = fmaxf(mv[0], mv[1]);
+      const float top = fmaxf(fmaxf(mv[0], mv[1]), mv[2]);
       float den = 0.f;
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
+      for (int e = 0; e < 3; ++e) {
         const float wt = mv[e] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv[e] - top);
         den += wt * lv[e];
         acc += wt * ov[e];
@@ -1161,7 +1175,8 @@ extern "C" size_t omni_beam_attention_workspace(int32_t groups, int32_t beams, i
                                                 int32_t ctx_keys, int32_t chunk) {
   if (groups <= 0 || beams <= 0 || heads <= 0 || head_dim <= 0 || ctx_keys <= 0) return 0;
   if (chunk <= 0) chunk = omni_verify_attention_chunk(groups, beams, heads, head_dim, ctx_keys);
-  const size_t splits = (size_t)attn_splits(ctx_keys, chunk) + 1;
+  size_t splits = (size_t)attn_splits(ctx_keys, chunk) + 1;
+  if (splits < 3) splits = 3;  // or the two context halves and the generated keys
   const size_t units = (size_t)groups * heads * splits * beams;
   return align256(units * head_dim * sizeof(float)) + align256(units * 2 * sizeof(float));
 }
@@ -1172,8 +1187,8 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
                                    int64_t gen_pos, int64_t gen_cap, int64_t gen_rows, const int32_t* ptr,
                                    int64_t ptr_stride, const int64_t* gen_len, int32_t groups, int32_t beams,
                                    int32_t heads, int32_t head_dim, int32_t ctx_keys, int32_t chunk, float scale,
-                                   void* out, void* workspace, size_t workspace_bytes, int32_t dtype,
-                                   void* stream) {
+                                   void* out, void* workspace, size_t workspace_bytes, int32_t* counters,
+                                   int32_t dtype, void* stream) {
   if (groups < 0 || ctx_keys <= 0 || ctx_cap <= 0 || gen_cap <= 0 || gen_rows <= 0) return OMNI_ERR_INVALID;
   int st = check_attention_shape(beams, heads, head_dim, dtype, scale);
   if (st != OMNI_OK) return st;
@@ -1191,7 +1206,7 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
   if (((uintptr_t)workspace & 255u) != 0) return OMNI_ERR_WORKSPACE;
   if (!attention_aligned(q, out, k_ctx, v_ctx, ctx_row, ctx_head, ctx_pos, head_dim, dtype)) return OMNI_ERR_INVALID;
   const int ctx_splits = attn_splits(ctx_keys, chunk);
-  const int splits = ctx_splits + 1;
+  const int splits = ctx_splits + 1 > 3 ? ctx_splits + 1 : 3;  // partial slots per unit (see the workspace)
   const size_t units = (size_t)groups * heads * splits * beams;
   AttnArgs a;
   a.q = q;
@@ -1217,8 +1232,18 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
   a.ctx_splits = ctx_splits;
   a.gen_split = ctx_splits;
   hipStream_t s = (hipStream_t)stream;
-  st = launch_attention(a, groups, dtype, s);
-  if (st != OMNI_OK) return st;
+  const bool halves = dtype == OMNI_BF16 && head_dim == 128 && ctx_pos == head_dim && beams <= kWgMaxT &&
+                      groups <= kPairMaxRows && counters != nullptr && (int64_t)groups * heads >= kWgMinUnits;
+  if (halves) {  // the generated keys' partial first, then the context halves, whose last merge includes it
+    a.chunk = (ctx_keys + 31) / 32 * 32;
+    a.ctx_splits = 1;
+    a.gen_split = 2;
+    a.splits = splits;  // >= 3 slots per unit (see omni_beam_attention_workspace)
+    a.counters = counters;
+  } else {
+    st = launch_attention(a, groups, dtype, s);
+    if (st != OMNI_OK) return st;
+  }
   BeamGenArgs gargs;
   gargs.q = q;
   gargs.kg = k_gen;
@@ -1237,12 +1262,17 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
   gargs.scale_log2 = a.scale_log2;
   gargs.part_o = a.part_o;
   gargs.part_ml = a.part_ml;
-  gargs.splits = splits;
-  gargs.gen_split = ctx_splits;
   dim3 ggrid(heads, groups * beams);
+  gargs.splits = a.splits;
+  gargs.gen_split = a.gen_split;
   if (dtype == OMNI_BF16) beam_gen_kernel<uint16_t><<<ggrid, 64, 0, s>>>(gargs);
   else beam_gen_kernel<float><<<ggrid, 64, 0, s>>>(gargs);
   st = omni_launch_status();
   if (st != OMNI_OK) return st;
+  if (halves) {
+    const size_t lds = (size_t)kWgWaves * beams * (head_dim + 2) * sizeof(float);
+    verify_attn_pair_kernel<128><<<groups * heads, 64 * kWgWaves, lds, s>>>(a, groups, a.splits);
+    return omni_launch_status();
+  }
   return launch_combine(a, groups, dtype, s);
 }

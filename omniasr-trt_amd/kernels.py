@@ -201,12 +201,14 @@ def beam_attention(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, ctx_len:
     _need(ctx_len.numel() >= groups and gen_len.numel() >= rows, "ctx_len: [S], gen_len: [S*N]")
     ws = lib.omni_beam_attention_workspace(groups, beams, heads, dim, ctx_keys, int(chunk))
     workspace = torch.empty(max(ws, 256), device=q.device, dtype=torch.uint8)
+    counters = _attn_counters(q.device, groups * heads)
     out = torch.empty_like(q)
     status = lib.omni_beam_attention(
         q.data_ptr(), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.size(2),
         ctx_len.data_ptr(), kg.data_ptr(), vg.data_ptr(), kg.stride(0), kg.stride(1), kg.stride(2), kg.size(2),
         kg.size(0), ptr.data_ptr(), ptr.stride(0), gen_len.data_ptr(), groups, beams, heads, dim, int(ctx_keys),
-        int(chunk), float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel(), _dtype(q), _stream(q))
+        int(chunk), float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel(), counters.data_ptr(),
+        _dtype(q), _stream(q))
     _lib.check(status, "beam attention")
     return out
 

@@ -85,6 +85,18 @@ def test_beam_attention_config5(cuda):
         _beam_case(cuda, torch.bfloat16, 8, 5, 32, 128, keys, 256, ctx_len, gen_len, keys, 56, BF16_TOL, chunk=chunk)
 
 
+@pytest.mark.parametrize("beams", [3, 5, 14])
+def test_beam_attention_context_halves(cuda, beams):
+    """8 inputs x 32 heads x 128: the context by balanced halves merged with the generated keys' partial -- finished
+    inputs (no context, no generated keys), a context shorter than a tile, generated keys only."""
+    g = torch.Generator().manual_seed(70 + beams)
+    ctx_len = torch.tensor([2300, 0, 17, 1500, 0, 640, 999, 33])
+    gen_len = torch.randint(0, 97, (8 * beams,), generator=g)
+    gen_len[beams: 2 * beams] = 0  # input 1 finished
+    keys = 2304
+    _beam_case(cuda, torch.bfloat16, 8, beams, 32, 128, keys, 96, ctx_len, gen_len, keys, 71, BF16_TOL)
+
+
 def test_beam_attention_graph_replays(cuda):
     """Captured once, replayed with new pointers and lengths written in place between replays."""
     q, kc, vc, kg, vg, ptr, cl, gl = _beam_inputs(torch.bfloat16, 4, 3, 8, 128, 512, 128, [500, 200, 37, 512],
@@ -110,6 +122,37 @@ def test_beam_attention_graph_replays(cuda):
         torch.cuda.synchronize()
         eager = kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr, gl, 3, 512, 128 ** -0.5)
         assert torch.equal(out, eager), rep
+
+
+def test_beam_attention_halves_graph_replays(cuda):
+    """The halves path (8 inputs x 5 beams x 32 heads) captured once and replayed with new lengths and pointers;
+    every replay equals the eager call bit for bit (the tickets are left zero between calls)."""
+    q, kc, vc, kg, vg, ptr, cl, gl = _beam_inputs(torch.bfloat16, 8, 5, 32, 128, 1024, 64,
+                                                  [1000, 0, 512, 77, 1024, 3, 640, 900],
+                                                  torch.randint(0, 65, (40,), generator=torch.Generator().manual_seed(5)),
+                                                  13)
+    q, kc, vc, kg, vg, ptr, cl, gl = (t.to(cuda) for t in (q, kc, vc, kg, vg, ptr, cl, gl))
+    kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr, gl, 5, 1024, 128 ** -0.5)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        graph.capture_begin()
+        out = kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr, gl, 5, 1024, 128 ** -0.5)
+        graph.capture_end()
+    torch.cuda.current_stream().wait_stream(stream)
+    g = torch.Generator(device=cuda).manual_seed(4)
+    for rep in range(4):
+        ptr.copy_(torch.randint(0, 42, ptr.shape, device=cuda, generator=g, dtype=torch.int32))
+        gl.copy_(torch.randint(0, 65, gl.shape, device=cuda, generator=g))
+        cl.copy_(torch.randint(0, 1025, cl.shape, device=cuda, generator=g))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr, gl, 5, 1024, 128 ** -0.5)
+        assert torch.equal(out, eager), rep
+    assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
 
 
 def test_beam_attention_rejects_bad_shapes(cuda):
