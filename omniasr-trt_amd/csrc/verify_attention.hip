@@ -1169,6 +1169,78 @@ __global__ __launch_bounds__(64) void beam_gen_kernel(BeamGenArgs a) {
   }
 }
 
+// The same for bf16 rows of 128 dimensions with both products' loads in one round trip: per pass of up to 64 keys
+// each lane loads its key's K row (16 x 16 bytes) and its share of the V rows (lanes 16g .. 16g + 15 read keys
+// g, g + 4, ..., 8 dimensions each) as soon as the pointers are in, before any score exists.
+__global__ __launch_bounds__(64) void beam_gen_kernel_d128(BeamGenArgs a) {
+  constexpr int D = 128, kRow = D / 8;  // 16 lanes read a row
+  __shared__ float qs[D];
+  __shared__ float ps[kWave];
+  __shared__ int64_t off_sh[kWave];
+  __shared__ float red[4 * D];
+  const int h = blockIdx.x, r = blockIdx.y;
+  const int lane = threadIdx.x, grp = lane / kRow, sub = lane - grp * kRow;
+  const int64_t n = clamp64(a.gen_len[r], 0, a.gen_cap);
+  const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * a.H + h) * D;
+  for (int d = lane; d < D; d += kWave) qs[d] = bf16_to_f32(qrow[d]) * a.scale_log2;
+  const char* kb = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(a.kg) + h * a.s_head);
+  const char* vb = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(a.vg) + h * a.s_head);
+  float m_run = -INFINITY, l_run = 0.f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int64_t j0 = 0; j0 < n; j0 += kWave) {
+    const int64_t j = j0 + lane;
+    const bool valid = j < n;
+    int64_t src = valid ? (int64_t)a.ptr[(int64_t)r * a.ptr_stride + j] : 0;
+    src = clamp64(src, 0, a.gen_rows - 1);
+    const int64_t off = (src * a.s_row + (valid ? j : 0) * a.s_pos) * 2;  // bytes; invalid lanes read key 0
+    off_sh[lane] = off;
+    __syncthreads();
+    u32x4_t kx[kRow], vx[kWave / 4];
+#pragma unroll
+    for (int c2 = 0; c2 < kRow; ++c2) kx[c2] = *reinterpret_cast<const u32x4_t*>(kb + off + c2 * 16);
+#pragma unroll
+    for (int ii = 0; ii < kWave / 4; ++ii)
+      vx[ii] = *reinterpret_cast<const u32x4_t*>(vb + off_sh[grp + 4 * ii] + sub * 16);
+    float sc = 0.f;
+#pragma unroll
+    for (int c2 = 0; c2 < kRow; ++c2) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sc = fmaf(qs[c2 * 8 + e], bf16x8_elem(kx[c2], e), sc);
+    }
+    sc = valid ? sc : -INFINITY;
+    const float m_new = fmaxf(m_run, wave_max(sc));
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // m_new is finite: key j0 is valid
+    const float pr = __builtin_amdgcn_exp2f(sc - m_new);
+    l_run = l_run * alpha + pr;
+    m_run = m_new;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+    ps[lane] = pr;  // 0 for the invalid keys
+    __syncthreads();
+    const int kend = (int)((n - j0) < kWave ? (n - j0) : kWave);
+#pragma unroll
+    for (int ii = 0; ii < kWave / 4; ++ii) {
+      const bool kv = grp + 4 * ii < kend;  // rows past the keys in use never reach the product (stale memory)
+      const float p = ps[grp + 4 * ii];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = kv ? fmaf(p, bf16x8_elem(vx[ii], e), acc[e]) : acc[e];
+    }
+    __syncthreads();
+  }
+  const float l_tot = wave_sum(l_run);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) red[grp * D + sub * 8 + e] = acc[e];
+  __syncthreads();
+  const int g = r / a.beams, i = r - g * a.beams;
+  const int64_t slot = (((int64_t)g * a.H + h) * a.splits + a.gen_split) * a.beams + i;
+  for (int d = lane; d < D; d += kWave) a.part_o[slot * D + d] = red[d] + red[D + d] + red[2 * D + d] + red[3 * D + d];
+  if (lane == 0) {
+    a.part_ml[slot * 2] = m_run;
+    a.part_ml[slot * 2 + 1] = l_tot;
+  }
+}
+
 }  // namespace omni
 
 extern "C" size_t omni_beam_attention_workspace(int32_t groups, int32_t beams, int32_t heads, int32_t head_dim,
@@ -1265,7 +1337,8 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
   dim3 ggrid(heads, groups * beams);
   gargs.splits = a.splits;
   gargs.gen_split = a.gen_split;
-  if (dtype == OMNI_BF16) beam_gen_kernel<uint16_t><<<ggrid, 64, 0, s>>>(gargs);
+  if (dtype == OMNI_BF16 && head_dim == 128 && gen_pos == head_dim) beam_gen_kernel_d128<<<ggrid, 64, 0, s>>>(gargs);
+  else if (dtype == OMNI_BF16) beam_gen_kernel<uint16_t><<<ggrid, 64, 0, s>>>(gargs);
   else beam_gen_kernel<float><<<ggrid, 64, 0, s>>>(gargs);
   st = omni_launch_status();
   if (st != OMNI_OK) return st;
