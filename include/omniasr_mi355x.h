@@ -97,10 +97,11 @@ size_t omni_verify_attention_workspace(int32_t rows, int32_t tokens, int32_t hea
  * ``workspace``: at least omni_verify_attention_workspace() bytes, 256-byte aligned, any content.
  * ``counters``: rows*heads int32, zero before the first call; every call leaves them zero (calls
  * that share them must not overlap in time).
- * Decomposition: with bf16, head_dim 128, contiguous key rows (stride_pos == head_dim), tokens <= 15 and
- * rows * heads >= 128, one workgroup of 8 waves per (head, row) merges its waves' partials in LDS (no
- * workspace traffic, one launch, ``chunk`` unused) unless ``flags`` has OMNI_ATTN_SPLIT_K; otherwise split-K
- * as above.
+ * Decomposition: with bf16, head_dim 128, contiguous key rows (stride_pos == head_dim), tokens <= 11,
+ * rows <= 256 and rows * heads >= 128, one launch of rows*heads 8-wave workgroups: workgroup i takes the
+ * first half of the i-th longest (head, row) and the second half of the i-th shortest, and the two halves
+ * of each unit merge through the workspace and ``counters`` (``chunk`` unused; results do not depend on
+ * timing).  Otherwise, or when ``flags`` has OMNI_ATTN_SPLIT_K, split-K as above.
  * bf16: head_dim a multiple of 128 (contiguous key rows) runs on MFMA, any other multiple of 8 on the vector
  * ALUs; f32: vector ALUs (fp32 products).  tokens: 1..16.
  */
@@ -128,7 +129,7 @@ size_t omni_beam_attention_workspace(int32_t groups, int32_t beams, int32_t head
  * clamped into [0, gen_rows).  out = softmax(q.k * scale) . v over both parts, fp32 accumulation; no
  * key at all gives zeros.  One pass over a group's context serves all of its beams (the kernels of
  * omni_verify_attention with every query over the same keys); the generated keys are read by a
- * pointer-chasing kernel into one more partial.  bf16, head_dim 128, contiguous key rows, beams <= 14 and
+ * pointer-chasing kernel into one more partial.  bf16, head_dim 128, contiguous key rows, beams <= 11 and
  * groups * heads >= 128: the context halves kernel merges that partial in its last step (``counters``:
  * groups*heads int32 tickets, zero before the first call, left zero); otherwise split-K and a merge launch.
  * ``chunk``: context keys per split (0: the library's choice).  ``workspace``: at least

@@ -290,8 +290,11 @@ __device__ __forceinline__ u32x4_t ld16(const char* p) { return *reinterpret_cas
 
 // One 32-key tile of K and V into MFMA operand layout.  Key rows are contiguous (D elements apart), so each load is
 // the wave-uniform tile base plus a 32-bit lane offset.  K rows past ``kmax`` (the last cache position, relative to
-// the tile's first key; 31 inside the cache) are read at kmax, and V rows at or past ``vstop`` (the end of the keys
-// in use, relative; 32 for a full tile) are zero, so stale memory never reaches the P V product.
+// the tile's first key; 31 inside the cache) are read at kmax; their scores are masked.  V rows at or past
+// ``vstop`` (the end of the keys in use, relative; 32 for a full tile, >= 1 for a tile that is attended) are read
+// at vstop - 1, a key in use: every query's probability of those keys is 0, and 0 times a finite value of a key in
+// use adds nothing (stale memory past the keys could hold NaN).  Only addresses are clamped, never loaded data, so
+// nothing waits for a tile's loads before its math.
 template <int D>
 __device__ __forceinline__ void load_tile_clamped(KVTile<D>& t, const char* kt, const char* vt, int kmax, int vstop,
                                                   int c, int g) {
@@ -304,15 +307,14 @@ __device__ __forceinline__ void load_tile_clamped(KVTile<D>& t, const char* kt, 
 #pragma unroll
     for (int s = 0; s < KVTile<D>::KS; ++s) t.k[mb][s] = ld16(kt + ko + s * 64);
   }
+  int vmax = vstop - 1 < kmax ? vstop - 1 : kmax;
+  vmax = vmax > 0 ? vmax : 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int rv = 8 * g + j;
-    const uint32_t vo = (uint32_t)(rv < kmax ? rv : kmax) * kRow + c * 16;
+    const uint32_t vo = (uint32_t)(rv < vmax ? rv : vmax) * kRow + c * 16;
 #pragma unroll
-    for (int gg = 0; gg < KVTile<D>::NG; ++gg) {
-      const u32x4_t x = ld16(vt + vo + gg * 256);
-      t.v[gg][j] = rv < vstop ? x : u32x4_t{0u, 0u, 0u, 0u};
-    }
+    for (int gg = 0; gg < KVTile<D>::NG; ++gg) t.v[gg][j] = ld16(vt + vo + gg * 256);
   }
 }
 
@@ -567,10 +569,11 @@ __global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(Attn
 // ---------------------------------------------------------------------------------------------- workgroup per row
 
 constexpr int kWgWaves = 8;
-constexpr int kWgMaxT = 14;  // the waves' partials and the row ranking stay within 64 KB of LDS
+constexpr int kWgMaxT = 11;  // the waves' states, the fetched partials and the ranking stay within 64 KB of LDS
 constexpr int64_t kWgMinUnits = 128;  // rows x heads from which one workgroup per (head, row) beats split-K
 
 constexpr int kPairMaxRows = 256;
+constexpr int64_t kPairMaxQueryRows = int64_t{1} << 30;  // query rows x heads: 32-bit row indices in the kernel
 
 // The row's tile count: 32-key tiles up to the keys its last query sees.
 __device__ __forceinline__ int row_tile_count(const AttnArgs& a, int b) {
@@ -578,22 +581,128 @@ __device__ __forceinline__ int row_tile_count(const AttnArgs& a, int b) {
   return (int)((r.total + 31) >> 5);
 }
 
-// One 8-wave workgroup per (head, row) unit, but working on halves: units are ranked by length, and workgroup i
-// takes the first half of the i-th longest unit and the second half of the i-th shortest, so the workgroups (one
-// per CU) stream about the same number of tiles.  That balance is what the HBM needs: a CU reads at most ~30 GB/s,
-// so the GPU streams at full rate only while nearly every CU is busy.  In each half the 8 waves take interleaved
-// tiles and merge in LDS; the half's partial is written through to the coherence point, and the second of a
-// unit's two halves to finish merges them (one round of loads) and writes the output.
+// Two floats x 2 (16 bytes) written through to the coherence point as two 8-byte agent-scope stores.  Unlike
+// put_through4 these are stores the compiler counts, so a later wait for older loads does not wait for them.
+__device__ __forceinline__ void put_through4c(float* p, f32x4_t v) {
+  put_through2(p, v[0], v[1]);
+  put_through2(p + 2, v[2], v[3]);
+}
+
+// One partial (m, l, O[t][d .. d + 3]) read at the coherence point.
+struct PartialItem {
+  float m, l;
+  f32x4_t o;
+};
+
+__device__ __forceinline__ PartialItem get_partial(const AttnArgs& a, int64_t slot_base, int t, int d) {
+  const uint64_t ml = __hip_atomic_load(reinterpret_cast<uint64_t*>(a.part_ml + (slot_base * a.T + t) * 2),
+                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return PartialItem{__uint_as_float((uint32_t)ml), __uint_as_float((uint32_t)(ml >> 32)),
+                     get_through4(a.part_o + (slot_base * a.T + t) * a.D + d)};
+}
+
+// Up to three partials of one output item merged and written (bf16).
+__device__ __forceinline__ void write_merged(const AttnArgs& a, int b, int h, int t, int d, const PartialItem (&p)[3],
+                                             int np) {
+  float top = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < 3; ++e) top = e < np ? fmaxf(top, p[e].m) : top;
+  float den = 0.f;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int e = 0; e < 3; ++e) {
+    const float wt = e >= np || p[e].m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(p[e].m - top);
+    den += wt * (e < np ? p[e].l : 0.f);
+    acc += wt * (e < np ? p[e].o : f32x4_t{0.f, 0.f, 0.f, 0.f});
+  }
+  const float div = den > 0.f ? den : 1.f;
+  store4<uint16_t>(reinterpret_cast<uint16_t*>(a.out) + (int64_t)((b * a.T + t) * a.H + h) * a.D + d, acc / div);
+}
+
+// The wave's n >= 1 tiles of one sequence: X holds (is loading) tile 0, Y is free.  Tile k + 1 loads while tile k's
+// math runs, and during the last tile's math ``ldn`` loads the next sequence's first tile.  Every load is
+// unconditional (the loop's own branches only), so each wait is for one tile's loads.  Returns 0 if the next
+// sequence's first tile is in X, 1 if in Y.
+template <int D, class LD, class AT, class LDN>
+__device__ __forceinline__ int run_tiles(KVTile<D>& X, KVTile<D>& Y, int n, LD ld, AT at, LDN ldn) {
+  int k = 0;
+  for (; k + 2 < n; k += 2) {
+    ld(Y, k + 1);
+    at(X, k);
+    ld(X, k + 2);
+    at(Y, k + 1);
+  }
+  if (k + 1 < n) {
+    ld(Y, k + 1);
+    at(X, k);
+    ldn(X);
+    at(Y, k + 1);
+    return 0;
+  }
+  ldn(Y);
+  at(X, k);
+  return 1;
+}
+
+// NS softmax states in LDS (NS x [T][D] O, [T] m, [T] l) merged into this thread's item (t, d) of a partial.
+template <int NS>
+__device__ __forceinline__ PartialItem merge_slots(const float* po, const float* pm, const float* pl, int T, int D,
+                                                   int t, int d) {
+  float top = -INFINITY;
+#pragma unroll
+  for (int v = 0; v < NS; ++v) top = fmaxf(top, pm[v * T + t]);
+  float den = 0.f;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int v = 0; v < NS; ++v) {
+    const float mv = pm[v * T + t];
+    const float wt = mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - top);
+    den += wt * pl[v * T + t];
+    acc += wt * *reinterpret_cast<const f32x4_t*>(po + (v * T + t) * D + d);
+  }
+  return PartialItem{top, den, acc};
+}
+
+// Unit tickets of the halves (one int per unit, zero between launches).  The first half's workgroup publishes its
+// partial, then adds kTicketFirst.  The second half's workgroup adds kTicketClaim before publishing anything: an
+// old value of kTicketFirst means the first half is out and it merges at once from its own registers.  Otherwise it
+// publishes its partial and adds kTicketSecond: an old value of kTicketClaim + kTicketFirst means the first half
+// came out in between and it merges; an old value of kTicketClaim means the first half's workgroup will find
+// kTicketClaim + kTicketSecond and merge.  Exactly one workgroup merges, after the last add, and it resets the
+// ticket to zero.
+constexpr int kTicketFirst = 1, kTicketClaim = 2, kTicketSecond = 4;
+
+// Dynamic LDS of the halves kernel: the waves' states, the two fetched partials of unit 1, half 1's queries (bf16).
+__host__ __device__ constexpr size_t pair_lds_bytes(int T, int D) {
+  return (size_t)(kWgWaves + 2) * T * (D + 2) * sizeof(float) + (size_t)T * D * 2;
+}
+
+// One 8-wave workgroup per (head, row) unit, working on halves: units are ranked by length, and workgroup i takes
+// the first half of the i-th longest unit ("half 0") and the second half of the i-th shortest ("half 1"), so the
+// workgroups (one per CU) stream about the same number of tiles.  That balance is what the HBM needs: a CU reads
+// at most ~30 GB/s, so the GPU streams at full rate only while nearly every CU is busy.
+//
+// The workgroup's tiles (half 0's, then half 1's) are dealt round-robin over its 8 waves in one sequence, and each
+// wave's tiles run through both halves in one pipeline (half 1's first tile loads during half 0's last).  At the
+// switch the waves' half-0 states merge in LDS and the partial is written through to the coherence point while the
+// next tiles load.  The first wave to finish half 1 claims unit 1 (see kTicketFirst) and, if its first half is out,
+// fetches it into LDS while the other waves finish, so the common end is an LDS merge and the output store.  The
+// dealing is static, so results do not depend on timing.
 template <int D>
 __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(AttnArgs a, int rows, int slots) {
-  constexpr int NG = D / 128;
-  extern __shared__ float smem[];  // [waves][T][D] partial outputs, [waves][T] m, [waves][T] l
+  static_assert(D == 128, "the halves kernel serves head dim 128");
+  constexpr int KS = D / 32;
+  constexpr int kFetched = kWgWaves;  // LDS state slots of the fetched partials: unit 1's first half, its generated keys
+  constexpr int kSlots = kWgWaves + 2;
+  extern __shared__ float smem[];  // [10][T][D] O, [10][T] m, [10][T] l, then [T][D] bf16 queries
   __shared__ int ntl[kPairMaxRows];
   __shared__ int order[kPairMaxRows];  // rows by tile count, longest first (ties: lower row first)
-  __shared__ int s_tickets[2];
+  __shared__ int s_tk[2];
+  __shared__ int s_done;  // waves done with their tiles
   const int tid = threadIdx.x, lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int T = a.T, H = a.H, U = rows * H;
+  if (tid == 0) s_done = 0;
   for (int b = tid; b < rows; b += 64 * kWgWaves) ntl[b] = row_tile_count(a, b);
   __syncthreads();
   for (int b = tid; b < rows; b += 64 * kWgWaves) {
@@ -604,107 +713,246 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
   }
   __syncthreads();
   const int i = blockIdx.x;
-  int unit[2];
-  unit[0] = order[i / H] * H + i % H;                      // the i-th longest unit: its first half
-  unit[1] = order[(U - 1 - i) / H] * H + (U - 1 - i) % H;  // the i-th shortest: its second half
+  const int u0 = __builtin_amdgcn_readfirstlane(order[i / H] * H + i % H);
+  const int u1 = __builtin_amdgcn_readfirstlane(order[(U - 1 - i) / H] * H + (U - 1 - i) % H);
+  const int b0 = u0 / H, h0 = u0 - b0 * H, b1 = u1 / H, h1 = u1 - b1 * H;
+  const SplitRange r0 = split_range(a, b0, 0), r1 = split_range(a, b1, 0);
+  const int nt0 = (int)((r0.total + 31) >> 5), nt1 = (int)((r1.total + 31) >> 5);
+  const int e0 = (nt0 + 1) >> 1, s1 = (nt1 + 1) >> 1;  // half 0: tiles [0, e0) of u0; half 1: [s1, nt1) of u1
+  // Wave w takes half 0's tiles w, w + 8, ...  Half 1's tiles go to waves 0..6 only (the last wave publishes half
+  // 0 at the switch), round-robin from wave e0 mod 8 on (the waves without an extra half-0 tile first): wave w < 7
+  // takes s1 + j1, s1 + j1 + 7, ..., j1 = (w - start) mod 7.
+  constexpr int kHalf1Waves = kWgWaves - 1;
+  const int start1 = e0 % kWgWaves < kHalf1Waves ? e0 % kWgWaves : 0;
+  const int j1 = ((w - start1) % kHalf1Waves + kHalf1Waves) % kHalf1Waves;
+  const int n0 = e0 > w ? (e0 - w + kWgWaves - 1) / kWgWaves : 0;
+  const int n1 = w < kHalf1Waves && nt1 - s1 > j1 ? (nt1 - s1 - j1 + kHalf1Waves - 1) / kHalf1Waves : 0;
+
   float* po = smem;
-  float* pm = smem + kWgWaves * T * D;
-  float* pl = pm + kWgWaves * T;
-  uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
+  float* pm = po + kSlots * T * D;
+  float* pl = pm + kSlots * T;
+  uint16_t* qs1 = reinterpret_cast<uint16_t*>(pl + kSlots * T);
+  const uint16_t* qg = reinterpret_cast<const uint16_t*>(a.q);
+  for (int idx = tid; idx < T * (D / 8); idx += 64 * kWgWaves) {
+    const int t = idx / (D / 8), d8 = (idx - t * (D / 8)) * 8;
+    *reinterpret_cast<u32x4_t*>(qs1 + t * D + d8) =
+        *reinterpret_cast<const u32x4_t*>(qg + (int64_t)((b1 * T + t) * H + h1) * D + d8);
+  }
+  // B operand of S^T = K Q^T for half 0: lane (c, g) holds q[c][32s + 8g .. 32s + 8g + 7].
+  u32x4_t qop[KS];
+  const u32x4_t zero = {0u, 0u, 0u, 0u};
+  {
+    const uint16_t* qrow = qg + (int64_t)((b0 * T + c) * H + h0) * D + g * 8;
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    const int u = unit[half], b = u / H, h = u - b * H;
-    SplitRange r = split_range(a, b, 0);
-    r.nact = kWgWaves;
-    const int64_t nt = (r.total + 31) >> 5, hm = (nt + 1) >> 1;
-    SoftmaxState st;
-    f32x4_t o[NG * 8];
-    attend_split<D, true>(a, b, h, w, r, st, o, half == 0 ? 0 : hm, half == 0 ? hm : nt);
+    for (int s = 0; s < KS; ++s) qop[s] = c < T ? *reinterpret_cast<const u32x4_t*>(qrow + s * 32) : zero;
+  }
+
+  const char* kb0 = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(a.k) + b0 * a.s_row + h0 * a.s_head);
+  const char* vb0 = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(a.v) + b0 * a.s_row + h0 * a.s_head);
+  const char* kb1 = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(a.k) + b1 * a.s_row + h1 * a.s_head);
+  const char* vb1 = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(a.v) + b1 * a.s_row + h1 * a.s_head);
+  const int64_t last_key = a.cache_len - 1;
+  // A tile of a unit's keys (see load_tile_clamped).  The launcher sends only caches with contiguous key rows
+  // (s_pos == D) here.
+  auto ld_tile = [&](KVTile<D>& t, const char* kb, const char* vb, int tile, int64_t total) {
+    const int64_t k0 = (int64_t)tile * 32;
+    const int64_t kmax = last_key - k0, vstop = total - k0;
+    load_tile_clamped<D>(t, kb + k0 * D * 2, vb + k0 * D * 2, kmax < 31 ? (int)kmax : 31,
+                         vstop < 32 ? (int)vstop : 32, c, g);
+  };
+  // Query c's key limit in the current half (keys fit in 32 bits); half 1's is set at the switch.
+  auto key_limit = [&](const SplitRange& r) {
+    const int64_t own = r.n + (a.causal ? c : 0);
+    return (int)(own < r.total ? own : r.total);
+  };
+  int lim = key_limit(r0);
+  const float c_scale = a.scale_log2;
+  SoftmaxState st{-INFINITY, -INFINITY, 0.f};
+  f32x4_t o[D / 16];
+#pragma unroll
+  for (int nb = 0; nb < D / 16; ++nb) o[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // The wave's k-th tile: the unit's base, tile index and key limit are scalar selects, so every load stays
+  // unconditional.
+  auto tile_of = [&](int k) { return k < n0 ? w + kWgWaves * k : s1 + j1 + kHalf1Waves * (k - n0); };
+  auto ld = [&](KVTile<D>& t, int k) {
+    const bool first = k < n0;
+    ld_tile(t, first ? kb0 : kb1, first ? vb0 : vb1, tile_of(k), first ? r0.total : r1.total);
+  };
+  auto flush = [&]() {
     float l_tot = st.l_run + __shfl_xor(st.l_run, 16, kWave);
     l_tot += __shfl_xor(l_tot, 32, kWave);
+    // The lane's LDS addresses are computed here, not kept in registers through the tile loops.
+    int lx = lane;
+    asm volatile("" : "+v"(lx));
+    const int fc = lx & 15, fg = lx >> 4;
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) {
-      const int t = 4 * g + ii;
+      const int t = 4 * fg + ii;
       if (t >= T) continue;
-#pragma unroll
-      for (int gg = 0; gg < NG; ++gg) {
-        f32x4_t* dst = reinterpret_cast<f32x4_t*>(po + (w * T + t) * D + gg * 128 + c * 8);
-        dst[0] = f32x4_t{o[gg * 8 + 0][ii], o[gg * 8 + 1][ii], o[gg * 8 + 2][ii], o[gg * 8 + 3][ii]};
-        dst[1] = f32x4_t{o[gg * 8 + 4][ii], o[gg * 8 + 5][ii], o[gg * 8 + 6][ii], o[gg * 8 + 7][ii]};
-      }
+      f32x4_t* dst = reinterpret_cast<f32x4_t*>(po + (w * T + t) * D + fc * 8);
+      dst[0] = f32x4_t{o[0][ii], o[1][ii], o[2][ii], o[3][ii]};
+      dst[1] = f32x4_t{o[4][ii], o[5][ii], o[6][ii], o[7][ii]};
     }
     if (g == 0 && c < T) {
       pm[w * T + c] = st.m_ref;
       pl[w * T + c] = l_tot;
     }
+  };
+  // Thread tid's item of a merged partial: query item_t, dimensions item_d .. item_d + 3 (T x D / 4 <= 352 items).
+  // Computed where used (from an opaque copy of tid), not kept in registers through the tile loops.
+  int item_t = 0, item_d = 0;
+  bool has_item = false;
+  auto set_item = [&]() {
+    int tx = tid;
+    asm volatile("" : "+v"(tx));
+    item_t = tx / (D / 4);
+    item_d = (tx - item_t * (D / 4)) * 4;
+    has_item = item_t < T;
+  };
+  // The switch, once per wave after its last half-0 tile (before its first tile if it has none): the waves' half-0
+  // states go to LDS; the last wave merges them, writes the partial through, waits for its stores and takes unit
+  // 0's first ticket (kept for the end), while the other waves go on with half 1's queries.
+  int tk0 = 0;
+  auto to_half1 = [&]() {
+    flush();
     __syncthreads();
-    float* gpo = a.part_o + ((int64_t)u * slots + half) * T * D;
-    float* gml = a.part_ml + ((int64_t)u * slots + half) * T * 2;
-    for (int idx = tid; idx < T * (D / 4); idx += 64 * kWgWaves) {
-      const int t = idx / (D / 4), d = (idx - t * (D / 4)) * 4;
-      float top = -INFINITY;
-#pragma unroll
-      for (int v = 0; v < kWgWaves; ++v) top = fmaxf(top, pm[v * T + t]);
-      float den = 0.f;
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int v = 0; v < kWgWaves; ++v) {
-        const float mv = pm[v * T + t];
-        const float wt = mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - top);
-        den += wt * pl[v * T + t];
-        acc += wt * *reinterpret_cast<const f32x4_t*>(po + (v * T + t) * D + d);
+    if (w == kWgWaves - 1) {
+      const int64_t sb = (int64_t)u0 * slots;
+      for (int idx = lane; idx < T * (D / 4); idx += kWave) {
+        const int t = idx / (D / 4), d = (idx - t * (D / 4)) * 4;
+        const PartialItem m0 = merge_slots<kWgWaves>(po, pm, pl, T, D, t, d);
+        put_through4c(a.part_o + (sb * T + t) * D + d, m0.o);
+        if (d == 0) put_through2(a.part_ml + (sb * T + t) * 2, m0.m, m0.l);
       }
-      put_through4(gpo + t * D + d, acc);
-      if (d == 0) put_through2(gml + t * 2, top, den);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(0);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      int v = 0;
+      if (lane == 0)
+        v = __hip_atomic_fetch_add(&a.counters[u0], kTicketFirst, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      tk0 = __builtin_amdgcn_readfirstlane(v);
     }
-    __syncthreads();  // the LDS partials are rewritten by the next half
-  }
-  // Both halves' partials have reached the coherence point: take the units' tickets; the second half of a unit
-  // to arrive merges the two.
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __syncthreads();
-  if (tid < 2) s_tickets[tid] = __hip_atomic_fetch_add(&a.counters[unit[tid]], 1, __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  // Beams: a third partial, the generated keys', written by the previous launch at slot gen_split.
-  const int nparts = a.gen_split >= 0 ? 3 : 2;
-  for (int q = 0; q < 2; ++q) {
-    if (s_tickets[q] != 1) continue;  // uniform over the workgroup
-    const int u = unit[q], b = u / H, h = u - b * H;
-    for (int idx = tid; idx < T * (D / 4); idx += 64 * kWgWaves) {
-      const int t = idx / (D / 4), d = (idx - t * (D / 4)) * 4;
-      float mv[3], lv[3];
-      f32x4_t ov[3];
+    st = SoftmaxState{-INFINITY, -INFINITY, 0.f};
 #pragma unroll
-      for (int e = 0; e < 3; ++e) {
-        mv[e] = -INFINITY;
-        lv[e] = 0.f;
-        ov[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        if (e < nparts) {
-          const int slot = e < 2 ? e : a.gen_split;
-          const float* ml = a.part_ml + (((int64_t)u * slots + slot) * T + t) * 2;
-          const uint64_t mlv = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(ml)),
-                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          mv[e] = __uint_as_float((uint32_t)mlv);
-          lv[e] = __uint_as_float((uint32_t)(mlv >> 32));
-          ov[e] = get_through4(a.part_o + (((int64_t)u * slots + slot) * T + t) * D + d);
+    for (int nb = 0; nb < D / 16; ++nb) o[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qop[s] = c < T ? *reinterpret_cast<const u32x4_t*>(qs1 + c * D + s * 32 + g * 8) : zero;
+    lim = key_limit(r1);
+  };
+  auto at = [&](const KVTile<D>& t, int k) {
+    attend<D>(t, qop, c_scale, st, o, g, tile_of(k) * 32 + 8 * g, lim);
+    if (k == n0 - 1) to_half1();
+  };
+  if (n0 == 0) to_half1();
+  const int n = n0 + n1;
+  if (n > 0) {
+    KVTile<D> A, B;
+    ld(A, 0);
+    run_tiles<D>(A, B, n, ld, at, [&](KVTile<D>&) {});
+  }
+
+  // ---- the end.  The first of waves 0..6 done claims unit 1 and, when its first half is out, copies it (and the
+  // beams' generated-keys partial) into the LDS slots kFetched, kFetched + 1 while the other waves finish.
+  const bool gen = a.gen_split >= 0;  // beams: a third partial, written by the previous launch at slot gen_split
+  if (w < kHalf1Waves) {
+    int first = 0;
+    if (lane == 0) first = __hip_atomic_fetch_add(&s_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (__builtin_amdgcn_readfirstlane(first) == 0) {
+      int tk = 0;
+      if (lane == 0)
+        tk = __hip_atomic_fetch_add(&a.counters[u1], kTicketClaim, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      tk = __builtin_amdgcn_readfirstlane(tk);
+      if (lane == 0) s_tk[1] = tk;
+      if (tk == kTicketFirst) {
+        constexpr int kRounds = (kWgMaxT * (D / 4) + kWave - 1) / kWave;
+        PartialItem p[kRounds][2];
+#pragma unroll
+        for (int r = 0; r < kRounds; ++r) {  // every load in flight at once
+          const int idx = lane + r * kWave, t = idx / (D / 4), d = (idx - t * (D / 4)) * 4;
+          if (t < T) {
+            p[r][0] = get_partial(a, (int64_t)u1 * slots, t, d);
+            if (gen) p[r][1] = get_partial(a, (int64_t)u1 * slots + a.gen_split, t, d);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < kRounds; ++r) {
+          const int idx = lane + r * kWave, t = idx / (D / 4), d = (idx - t * (D / 4)) * 4;
+          if (t < T) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              if (e == 1 && !gen) continue;
+              const int sl = kFetched + e;
+              *reinterpret_cast<f32x4_t*>(po + (sl * T + t) * D + d) = p[r][e].o;
+              if (d == 0) {
+                pm[sl * T + t] = p[r][e].m;
+                pl[sl * T + t] = p[r][e].l;
+              }
+            }
+          }
         }
       }
-      const float top = fmaxf(fmaxf(mv[0], mv[1]), mv[2]);
-      float den = 0.f;
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int e = 0; e < 3; ++e) {
-        const float wt = mv[e] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv[e] - top);
-        den += wt * lv[e];
-        acc += wt * ov[e];
-      }
-      const float div = den > 0.f ? den : 1.f;
-      store4<uint16_t>(out + ((int64_t)(b * T + t) * H + h) * D + d, acc / div);
     }
-    if (tid == 0) __hip_atomic_store(&a.counters[u], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();  // the last wave is done with half 0's states; the fetched slots are written
+  flush();
+  if (w == kWgWaves - 1 && lane == 0) s_tk[0] = tk0;
+  __syncthreads();
+  const int tk1 = s_tk[1];
+  set_item();
+  // Every merger of a unit combines (first half, second half, generated keys) in that order with the same
+  // arithmetic, so the output does not depend on which workgroup merges.
+  if (tk1 == kTicketFirst) {  // unit 1: the fetched first half + the waves' second half (+ generated keys)
+    if (has_item) {
+      PartialItem p[3];
+      p[0] = merge_slots<1>(po + kFetched * T * D, pm + kFetched * T, pl + kFetched * T, T, D, item_t, item_d);
+      p[1] = merge_slots<kWgWaves>(po, pm, pl, T, D, item_t, item_d);
+      p[2] = p[1];
+      if (gen)
+        p[2] = merge_slots<1>(po + (kFetched + 1) * T * D, pm + (kFetched + 1) * T, pl + (kFetched + 1) * T, T, D,
+                              item_t, item_d);
+      write_merged(a, b1, h1, item_t, item_d, p, gen ? 3 : 2);
+    }
+    if (tid == 0) __hip_atomic_store(&a.counters[u1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {  // half 1 claimed first: publish it, then the second add decides who merges
+    PartialItem m1{-INFINITY, 0.f, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+    if (has_item) {
+      m1 = merge_slots<kWgWaves>(po, pm, pl, T, D, item_t, item_d);
+      const int64_t sb = (int64_t)u1 * slots + 1;
+      put_through4c(a.part_o + (sb * T + item_t) * D + item_d, m1.o);
+      if (item_d == 0) put_through2(a.part_ml + (sb * T + item_t) * 2, m1.m, m1.l);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (tid == 0) s_tk[1] = __hip_atomic_fetch_add(&a.counters[u1], kTicketSecond, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_tk[1] == kTicketClaim + kTicketFirst) {  // the first half came out in between: merge here
+      if (has_item) {
+        PartialItem p[3];
+        p[0] = get_partial(a, (int64_t)u1 * slots, item_t, item_d);
+        p[1] = m1;
+        p[2] = m1;
+        if (gen) p[2] = get_partial(a, (int64_t)u1 * slots + a.gen_split, item_t, item_d);
+        write_merged(a, b1, h1, item_t, item_d, p, gen ? 3 : 2);
+      }
+      if (tid == 0) __hip_atomic_store(&a.counters[u1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+  if (s_tk[0] == kTicketClaim + kTicketSecond) {  // unit 0: both halves published
+    if (has_item) {
+      PartialItem p[3];
+      p[0] = get_partial(a, (int64_t)u0 * slots, item_t, item_d);
+      p[1] = get_partial(a, (int64_t)u0 * slots + 1, item_t, item_d);
+      p[2] = p[1];
+      if (gen) p[2] = get_partial(a, (int64_t)u0 * slots + a.gen_split, item_t, item_d);
+      write_merged(a, b0, h0, item_t, item_d, p, gen ? 3 : 2);
+    }
+    if (tid == 0) __hip_atomic_store(&a.counters[u0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1032,14 +1280,15 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
   a.gen_split = -1;
   hipStream_t s = (hipStream_t)stream;
   const bool wg = dtype == OMNI_BF16 && head_dim == 128 && stride_pos == head_dim && tokens <= kWgMaxT &&
-                  rows <= kPairMaxRows && !(flags & OMNI_ATTN_SPLIT_K) && (int64_t)rows * heads >= kWgMinUnits;
+                  rows <= kPairMaxRows && !(flags & OMNI_ATTN_SPLIT_K) && (int64_t)rows * heads >= kWgMinUnits &&
+                  (int64_t)rows * tokens * heads < kPairMaxQueryRows;
   if (wg) {  // one workgroup per (head, row): the whole key range is one split of kWgWaves waves
     a.chunk = (keys + 31) / 32 * 32;
     a.ctx_splits = 1;
     a.splits = 1;
     const int slots = (int)attn_slots(keys, chunk);
-    const size_t lds = (size_t)kWgWaves * tokens * (head_dim + 2) * sizeof(float);
-    verify_attn_pair_kernel<128><<<rows * heads, 64 * kWgWaves, lds, s>>>(a, rows, slots);
+    verify_attn_pair_kernel<128><<<rows * heads, 64 * kWgWaves, pair_lds_bytes(tokens, head_dim), s>>>(a, rows,
+                                                                                                     slots);
     return omni_launch_status();
   }
   st = launch_attention(a, rows, dtype, s);
@@ -1305,7 +1554,8 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
   a.gen_split = ctx_splits;
   hipStream_t s = (hipStream_t)stream;
   const bool halves = dtype == OMNI_BF16 && head_dim == 128 && ctx_pos == head_dim && beams <= kWgMaxT &&
-                      groups <= kPairMaxRows && counters != nullptr && (int64_t)groups * heads >= kWgMinUnits;
+                      groups <= kPairMaxRows && counters != nullptr && (int64_t)groups * heads >= kWgMinUnits &&
+                      (int64_t)groups * beams * heads < kPairMaxQueryRows;
   if (halves) {  // the generated keys' partial first, then the context halves, whose last merge includes it
     a.chunk = (ctx_keys + 31) / 32 * 32;
     a.ctx_splits = 1;
@@ -1343,8 +1593,8 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
   st = omni_launch_status();
   if (st != OMNI_OK) return st;
   if (halves) {
-    const size_t lds = (size_t)kWgWaves * beams * (head_dim + 2) * sizeof(float);
-    verify_attn_pair_kernel<128><<<groups * heads, 64 * kWgWaves, lds, s>>>(a, groups, a.splits);
+    verify_attn_pair_kernel<128><<<groups * heads, 64 * kWgWaves, pair_lds_bytes(beams, head_dim), s>>>(a, groups,
+                                                                                                         a.splits);
     return omni_launch_status();
   }
   return launch_combine(a, groups, dtype, s);

@@ -85,10 +85,11 @@ def test_beam_attention_config5(cuda):
         _beam_case(cuda, torch.bfloat16, 8, 5, 32, 128, keys, 256, ctx_len, gen_len, keys, 56, BF16_TOL, chunk=chunk)
 
 
-@pytest.mark.parametrize("beams", [3, 5, 14])
+@pytest.mark.parametrize("beams", [3, 5, 11, 12])
 def test_beam_attention_context_halves(cuda, beams):
-    """8 inputs x 32 heads x 128: the context by balanced halves merged with the generated keys' partial -- finished
-    inputs (no context, no generated keys), a context shorter than a tile, generated keys only."""
+    """8 inputs x 32 heads x 128: the context by balanced halves merged with the generated keys' partial (beams <= 11;
+    12 takes split-K) -- finished inputs (no context, no generated keys), a context shorter than a tile, generated keys
+    only."""
     g = torch.Generator().manual_seed(70 + beams)
     ctx_len = torch.tensor([2300, 0, 17, 1500, 0, 640, 999, 33])
     gen_len = torch.randint(0, 97, (8 * beams,), generator=g)

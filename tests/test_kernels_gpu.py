@@ -133,10 +133,10 @@ def test_verify_attention_config3(cuda, t):
     _attn_case(cuda, torch.bfloat16, 8, 32, 128, t, keys, lengths, keys, 1003, BF16_TOL)
 
 
-@pytest.mark.parametrize("t", [1, 5, 9, 15, 16])
+@pytest.mark.parametrize("t", [1, 5, 9, 11, 12, 16])
 def test_verify_attention_workgroup_and_split_k(cuda, t):
-    """8 rows x 32 heads: one 8-wave workgroup per (head, row) (T <= 15) and split-K on the same inputs, both
-    against the oracle; rows shorter than one tile per wave, empty, and ending inside a tile."""
+    """8 rows x 32 heads: the halves kernel (T <= 11) and split-K on the same inputs, both against the oracle; rows
+    shorter than one tile per wave, empty, and ending inside a tile."""
     lengths = torch.tensor([2400, 0, 31, 257, 1023, 7, 1800, 96])
     keys = -(-(int(lengths.max()) + t) // 256) * 256
     a = _attn_case(cuda, torch.bfloat16, 8, 32, 128, t, keys, lengths, keys, 31 + t, BF16_TOL)
