@@ -216,8 +216,9 @@ def time_attention(pkg, torch, dec, t: int, reps: int, seed: int = 1003, separat
 
 
 def time_small_kernels(pkg, torch, dec, reps: int = 200) -> dict:
-    """Config 2 RoPE + append (decode size and the 8 x 2048 prefill size), the fused argmax + acceptance and the
-    proposal, each timed with HIP events over ``reps`` launches (latency-bound at decode sizes)."""
+    """Config 2 RoPE + append (decode size and the 8 x 2048 prefill size), the causal prefill attention (8 x 2048),
+    the fused argmax + acceptance and the proposal, each timed with HIP events over ``reps`` launches
+    (latency-bound at decode sizes)."""
     kernels, spec = pkg.kernels, pkg.spec
     res = {}
     heads, dim = dec.heads, dec.head_dim
@@ -250,6 +251,17 @@ def time_small_kernels(pkg, torch, dec, reps: int = 200) -> dict:
         us = timed(lambda: kernels.rope_kv(qkv, cs, pos, kc, vc, heads, slots), reps if n < 1000 else 20)
         nbytes = n * (3 * heads * dim * 2 + dim // 2 * 2 * 4 + 3 * heads * dim * 2 + 16)
         res[name] = {"us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1)}
+    # Causal prefill attention of 8 contexts of 2048 positions over the cache rows just written (MFMA-bound):
+    # 4 * D flops per (query, visible key) pair per head.
+    width = 2048
+    q = torch.randn(SLOTS * width, heads, dim, device="cuda", generator=g).to(torch.bfloat16)
+    kc.normal_(generator=g)
+    vc.normal_(generator=g)
+    rows = torch.arange(SLOTS, device="cuda")
+    us = timed(lambda: kernels.prefill_attention(q, kc, vc, rows, width, dim ** -0.5), 10)
+    flops = 4 * dim * heads * SLOTS * width * (width + 1) // 2
+    res["prefill_attention_8x2048"] = {"us": round(us, 2), "flops": flops, "TFLOPs": round(flops / us / 1e6, 1),
+                                       "frac_bf16_peak": round(flops / us / 1e6 / 2500.0, 4)}
     v = dec.m.final_proj.weight.size(0)
     logits = torch.randn(SLOTS * (DRAFT + 1), v, device="cuda", generator=g).to(torch.bfloat16)
     tokens = torch.randint(3, v, (SLOTS, DRAFT + 1), device="cuda", generator=g)

@@ -145,6 +145,21 @@ int omni_beam_attention(const void *q, const void *k_ctx, const void *v_ctx, int
                         int32_t dtype, void *stream);
 
 /*
+ * Causal attention over whole contexts: the prefill's
+ *     F.scaled_dot_product_attention(q, k, v, is_causal=True)
+ * (src/omniasr_trt/decode.py:163-164, after kernels.rope_kv has written the contexts' K / V into their cache
+ * rows, decode.py:155-162).  Query p (0 <= p < width) of context b attends to keys [0, p] of cache row
+ * slots[b] (clamped into [0, cache_rows)); q and out are [contexts * width, heads, head_dim] (context b's
+ * queries at rows b*width .. b*width + width - 1, right padding computed like any other position).
+ * K / V caches: element strides stride_row / stride_head / stride_pos, cache_len >= width positions.
+ * bf16, head_dim 128, contiguous key rows (stride_pos == head_dim); fp32 accumulation.  No workspace.
+ */
+int omni_prefill_attention(const void *q, const void *k_cache, const void *v_cache, int64_t stride_row,
+                           int64_t stride_head, int64_t stride_pos, int64_t cache_len, int64_t cache_rows,
+                           const int64_t *slots, int32_t contexts, int32_t width, int32_t heads,
+                           int32_t head_dim, float scale, void *out, int32_t dtype, void *stream);
+
+/*
  * Draft proposal of every row.  Replaces ``kernels.propose`` / ``_propose``
  * (src/omniasr_trt/kernels.py:361-377, 214-268) as called by ``SpecDecoder.propose``
  * (src/omniasr_trt/spec.py:76-80).

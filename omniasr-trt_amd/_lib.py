@@ -36,6 +36,8 @@ _SIGNATURES = {
     "omni_beam_attention": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, c_int64, c_int64,
                                     c_int64, c_int64, c_int64, _P, c_int64, _P, c_int32, c_int32, c_int32, c_int32,
                                     c_int32, c_int32, c_float, _P, _P, c_size_t, _P, c_int32, _P]),
+    "omni_prefill_attention": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, _P, c_int32, c_int32,
+                                       c_int32, c_int32, c_float, _P, c_int32, _P]),
     "omni_propose": (c_int, [_P, c_int64, c_int64, _P, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int32,
                              c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, _P, _P]),
     "omni_spec_prepare": (c_int, [_P, c_int64, c_int64, _P, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int32,

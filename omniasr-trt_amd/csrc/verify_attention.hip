@@ -1599,3 +1599,150 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
   }
   return launch_combine(a, groups, dtype, s);
 }
+
+// ---------------------------------------------------------------------------------------------- prefill (causal)
+
+namespace omni {
+
+// Causal attention over whole contexts (the prefill): query p of context b attends to keys [0, p] of its cache row.
+// One workgroup of kPfWaves waves per (64-query block, head, context); the block's 32-key tiles go through LDS once
+// for all of its waves (double-buffered: tile t + 1's global loads are in flight during tile t's math), and each
+// wave runs the verify kernels' tile math (S^T = K Q^T, lazy softmax, O += P V on MFMA) for its 16 queries, with
+// the causal limit as the per-query key limit.  Tiles wholly past a wave's last query are skipped by that wave.
+constexpr int kPfWaves = 4;
+constexpr int kPfQueries = 16 * kPfWaves;
+constexpr int kPfRow = 128 * 2 + 16;  // LDS bytes per key row: 256 B of data, padded against bank conflicts
+
+struct PrefillArgs {
+  const uint16_t* q;    // [B * width, H, 128] bf16
+  const uint16_t* k;    // cache rows: element strides s_row / s_head, key rows contiguous (128 elements)
+  const uint16_t* v;
+  const int64_t* slots;  // [B] cache row of each context
+  int64_t s_row, s_head, cache_rows;
+  int width, H;
+  float scale_log2;
+  uint16_t* out;  // [B * width, H, 128] bf16
+};
+
+__global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(PrefillArgs a) {
+  constexpr int D = 128, KS = D / 32;
+  __shared__ __attribute__((aligned(16))) char lds[2][2][32 * kPfRow];  // [buffer][K, V][key rows]
+  const int nqb = (a.width + kPfQueries - 1) / kPfQueries;
+  const int qb = (nqb - 1 - (int)blockIdx.x) * kPfQueries;  // the longest blocks first
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q0 = qb + 16 * w;  // this wave's first query
+  const int64_t slot = clamp64(a.slots[b], 0, a.cache_rows - 1);
+  const uint16_t* kbase = a.k + slot * a.s_row + h * a.s_head;
+  const uint16_t* vbase = a.v + slot * a.s_row + h * a.s_head;
+  const int kend = min(qb + kPfQueries, a.width);  // keys the block's last query sees
+  const int nt = (kend + 31) >> 5;
+
+  // Global -> LDS: thread tid moves 16-byte chunks tid and tid + 256 of the tile's K and of its V (32 rows x 256 B
+  // each).  Rows past the context read its last key (finite: masked by the causal limit, never NaN).
+  u32x4_t stage[4];
+  auto fetch = [&](int t) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int ci = tid + e * 256, r = ci >> 4, col = ci & 15;
+      const int key = min(t * 32 + r, a.width - 1);
+      stage[e] = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)key * D + col * 8);
+      stage[2 + e] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)key * D + col * 8);
+    }
+  };
+  auto put = [&](int buf) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int ci = tid + e * 256, r = ci >> 4, col = ci & 15;
+      *reinterpret_cast<u32x4_t*>(&lds[buf][0][r * kPfRow + col * 16]) = stage[e];
+      *reinterpret_cast<u32x4_t*>(&lds[buf][1][r * kPfRow + col * 16]) = stage[2 + e];
+    }
+  };
+
+  // B operand of S^T = K Q^T: lane (c, g) holds q[q0 + c][32s + 8g .. 32s + 8g + 7] (0 past the context).
+  u32x4_t qop[KS];
+  {
+    const bool live = q0 + c < a.width;
+    const uint16_t* qrow = a.q + ((int64_t)(b * a.width + (live ? q0 + c : 0)) * a.H + h) * D + g * 8;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qop[s] = live ? *reinterpret_cast<const u32x4_t*>(qrow + s * 32) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+  SoftmaxState st{-INFINITY, -INFINITY, 0.f};
+  f32x4_t o[D / 16];
+#pragma unroll
+  for (int nb = 0; nb < D / 16; ++nb) o[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int lim = q0 + c + 1;  // query q0 + c sees keys [0, q0 + c]
+
+  fetch(0);
+  put(0);
+  __syncthreads();
+  for (int t = 0; t < nt; ++t) {
+    fetch(t + 1 < nt ? t + 1 : t);  // unconditional: the last iteration re-reads its own tile (cache hit)
+    if (q0 < a.width && t * 32 <= q0 + 15) {  // some query of this wave sees the tile
+      const char* kl = lds[t & 1][0];
+      const char* vl = lds[t & 1][1];
+      KVTile<D> tile;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const int rk = 8 * (c >> 2) + 4 * mb + (c & 3);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) tile.k[mb][s] = *reinterpret_cast<const u32x4_t*>(kl + rk * kPfRow + g * 16 + s * 64);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) tile.v[0][j] = *reinterpret_cast<const u32x4_t*>(vl + (8 * g + j) * kPfRow + c * 16);
+      attend<D>(tile, qop, a.scale_log2, st, o, g, t * 32 + 8 * g, lim);
+    }
+    put((t + 1) & 1);
+    __syncthreads();
+  }
+
+  // ---- the wave's 16 output rows: O / l, rounded to bf16
+  float l_tot = st.l_run + __shfl_xor(st.l_run, 16, kWave);
+  l_tot += __shfl_xor(l_tot, 32, kWave);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float li = __shfl(l_tot, 4 * g + i, kWave);
+    const int qq = q0 + 4 * g + i;
+    if (qq >= a.width) continue;
+    const float div = li > 0.f ? li : 1.f;
+    u32x4_t wv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wv[e] = pack_bf16x2(o[2 * e][i] / div, o[2 * e + 1][i] / div);
+    *reinterpret_cast<u32x4_t*>(a.out + ((int64_t)(b * a.width + qq) * a.H + h) * D + c * 8) = wv;
+  }
+}
+
+}  // namespace omni
+
+extern "C" int omni_prefill_attention(const void* q, const void* k_cache, const void* v_cache, int64_t stride_row,
+                                      int64_t stride_head, int64_t stride_pos, int64_t cache_len,
+                                      int64_t cache_rows, const int64_t* slots, int32_t contexts, int32_t width,
+                                      int32_t heads, int32_t head_dim, float scale, void* out, int32_t dtype,
+                                      void* stream) {
+  if (contexts < 0 || width < 0 || heads <= 0 || cache_rows <= 0) return OMNI_ERR_INVALID;
+  if (dtype != OMNI_BF16) return OMNI_ERR_DTYPE;
+  if (head_dim != 128 || stride_pos != head_dim) return OMNI_ERR_SHAPE;
+  if (!(scale > 0.f) || width > cache_len) return OMNI_ERR_INVALID;
+  if (contexts == 0 || width == 0) return OMNI_OK;
+  if (!q || !k_cache || !v_cache || !slots || !out) return OMNI_ERR_INVALID;
+  if (!attention_aligned(q, out, k_cache, v_cache, stride_row, stride_head, stride_pos, head_dim, dtype))
+    return OMNI_ERR_INVALID;
+  if ((int64_t)contexts * width * heads >= (int64_t{1} << 31) / 128) return OMNI_ERR_INVALID;
+  omni::PrefillArgs a;
+  a.q = (const uint16_t*)q;
+  a.k = (const uint16_t*)k_cache;
+  a.v = (const uint16_t*)v_cache;
+  a.slots = slots;
+  a.s_row = stride_row;
+  a.s_head = stride_head;
+  a.cache_rows = cache_rows;
+  a.width = width;
+  a.H = heads;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.out = (uint16_t*)out;
+  dim3 grid((width + omni::kPfQueries - 1) / omni::kPfQueries, heads, contexts);
+  omni::prefill_attn_kernel<<<grid, 64 * omni::kPfWaves, 0, (hipStream_t)stream>>>(a);
+  return omni_launch_status();
+}

@@ -139,8 +139,9 @@ class GreedyDecoder:
 
     def prefill_into(self, ctx: list[Tensor], slots, k_cache: Tensor, v_cache: Tensor) -> Tensor:
         """Contexts into rows ``slots`` of ``k_cache`` / ``v_cache`` ([layers, rows, H, S, Dh]) -- RoPE and the cache
-        writes by ``kernels.rope_kv``, causal attention over each context in fp32; returns the log-softmax after each
-        context's last token [B, V] (model dtype).  (src/omniasr_trt/decode.py:137-179)"""
+        writes by ``kernels.rope_kv``, causal attention over each context by ``kernels.prefill_attention`` (bf16, head
+        dim 128; fp32 torch attention otherwise); returns the log-softmax after each context's last token [B, V]
+        (model dtype).  (src/omniasr_trt/decode.py:137-179)"""
         m, b = self.m, len(ctx)
         lens = [c.size(0) for c in ctx]
         width = max(lens)
@@ -150,18 +151,24 @@ class GreedyDecoder:
             x[j, : lens[j]] = c
         h = x.view(b * width, -1)
         pos = torch.arange(width, device=self.device).repeat(b)
-        slot = (torch.arange(b, device=self.device) if rows is None else rows).repeat_interleave(width)
+        ctx_rows = torch.arange(b, device=self.device) if rows is None else rows
+        slot = ctx_rows.repeat_interleave(width)
+        fused = kernels.prefill_supported(self.dtype, self.head_dim)
         for i, layer in enumerate(m.llama_decoder.layers):
             qkv_w, out_w, gi_w, ffo_w = self.layers[i]
             qkv = layer.self_attn_layer_norm(h) @ qkv_w.t()
             q = kernels.rope_kv(qkv, m.rope, pos, k_cache[i], v_cache[i], self.heads, slot)
-            q = q.view(b, width, self.heads, -1).transpose(1, 2)
-            k = k_cache[i, :b, :, :width] if rows is None else k_cache[i, rows, :, :width]
-            v = v_cache[i, :b, :, :width] if rows is None else v_cache[i, rows, :, :width]
-            # Right padding and causal attention: no valid token sees a pad.  fp32 math keeps bf16 batched
-            # products (and their transposed operands) out of this path.
-            o = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True).to(self.dtype)
-            h = torch.addmm(h, o.transpose(1, 2).reshape(b * width, -1), out_w.t())
+            # Right padding and causal attention: no valid token sees a pad.
+            if fused:  # bf16, head dim 128: the causal HIP kernel over the cache rows just written
+                o = kernels.prefill_attention(q, k_cache[i], v_cache[i], ctx_rows, width, self.head_dim ** -0.5)
+                o = o.view(b * width, -1)
+            else:  # fp32 math keeps bf16 batched products (and their transposed operands) out of this path
+                q = q.view(b, width, self.heads, -1).transpose(1, 2)
+                k = k_cache[i, :b, :, :width] if rows is None else k_cache[i, rows, :, :width]
+                v = v_cache[i, :b, :, :width] if rows is None else v_cache[i, rows, :, :width]
+                o = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True).to(self.dtype)
+                o = o.transpose(1, 2).reshape(b * width, -1)
+            h = torch.addmm(h, o, out_w.t())
             gate, inner = (layer.ffn_layer_norm(h) @ gi_w.t()).chunk(2, -1)
             h = torch.addmm(h, inner * F.silu(gate), ffo_w.t())
         h = h.view(b, width, -1)

@@ -213,6 +213,39 @@ def beam_attention(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, ctx_len:
     return out
 
 
+def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, slots: torch.Tensor,
+                      width: int, scale: float) -> torch.Tensor:
+    """Causal attention of whole contexts over their cache rows: ``q`` [B*width, H, 128] bf16 (context b's queries
+    at rows b*width ..), ``k_cache``/``v_cache`` [rows, H, S >= width, 128] bf16 with unit stride in D, ``slots`` [B]
+    the contexts' cache rows; query p of context b attends to keys [0, p] of row ``slots[b]``.  Returns
+    [B*width, H, 128] -- ``F.scaled_dot_product_attention(q, k, v, is_causal=True)`` of the prefill
+    (src/omniasr_trt/decode.py:163-164), in the query layout of :func:`rope_kv`."""
+    lib = _lib.load()
+    rows, heads, dim = q.shape
+    _need(width > 0 and rows % width == 0, "q: [B*width, H, D]")
+    contexts = rows // width
+    _need(q.is_contiguous(), "q: contiguous [B*width, H, D]")
+    _need(k_cache.dtype == q.dtype == v_cache.dtype, "q and the caches: one dtype")
+    _need(k_cache.stride() == v_cache.stride() and k_cache.shape == v_cache.shape, "k_cache / v_cache: same layout")
+    _need(k_cache.dim() == 4 and k_cache.stride(3) == 1 and k_cache.size(3) == dim and k_cache.size(1) == heads,
+          "caches: [rows, H, S, D] with unit stride in D")
+    _need(k_cache.size(2) >= width, "caches: at least width positions")
+    _index(slots, "slots")
+    _need(slots.numel() >= contexts, "slots: [B]")
+    out = torch.empty_like(q)
+    status = lib.omni_prefill_attention(
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
+        k_cache.stride(2), k_cache.size(2), k_cache.size(0), slots.data_ptr(), contexts, int(width), heads, dim,
+        float(scale), out.data_ptr(), _dtype(q), _stream(q))
+    _lib.check(status, "prefill attention")
+    return out
+
+
+def prefill_supported(dtype: torch.dtype, head_dim: int) -> bool:
+    """Whether :func:`prefill_attention` covers this element type and head size (bf16, 128)."""
+    return dtype == torch.bfloat16 and head_dim == 128
+
+
 def splits_for(rows: int, heads: int, keys: int, block: int = 64, programs: int = 264) -> tuple[int, int]:
     """Key splits (a power of two, about ``programs`` programs in all) and the keys each split covers -- the
     reference's rule for its Triton launches (src/omniasr_trt/kernels.py:393-400), kept for callers that use it;

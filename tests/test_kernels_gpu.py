@@ -117,6 +117,36 @@ def test_verify_attention_bf16(cuda, t):
     _attn_case(cuda, torch.bfloat16, 4, 8, 512, t, 700, lengths, 640, 3, BF16_TOL)
 
 
+@pytest.mark.parametrize("width", [1, 15, 64, 97, 300])
+def test_prefill_attention(cuda, width):
+    """Causal attention over whole contexts (src/omniasr_trt/decode.py:163-164) against the oracle's verify attention
+    with query p of a context over keys [0, p]: cache rows addressed through slots, widths that are not multiples
+    of the 64-query block or the 32-key tile."""
+    g = gen(60 + width)
+    b, h, d, rows, cap = 3, 4, 128, 5, 320
+    kc = torch.randn(rows, h, cap, d, generator=g).to(torch.bfloat16)
+    vc = torch.randn(rows, h, cap, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(b * width, h, d, generator=g).to(torch.bfloat16)
+    slots = torch.tensor([4, 0, 2])
+    say(f"prefill attention width={width}")
+    out = kernels.prefill_attention(q.to(cuda), kc.to(cuda), vc.to(cuda), slots.to(cuda), width, d ** -0.5)
+    torch.cuda.synchronize()
+    sl = slots.numpy()
+    want = ov.verify_attention(npf(q), npf(kc)[sl], npf(vc)[sl], np.ones(b, np.int64), width, d ** -0.5)
+    np.testing.assert_allclose(npf(out), want, atol=BF16_TOL[0], rtol=BF16_TOL[1])
+
+
+def test_prefill_attention_rejects_bad_shapes(cuda):
+    q = torch.zeros(2 * 8, 2, 128, dtype=torch.bfloat16, device=cuda)
+    kc = torch.zeros(2, 2, 8, 128, dtype=torch.bfloat16, device=cuda)
+    slots = torch.arange(2, device=cuda)
+    with pytest.raises(ValueError):  # more positions than the cache holds
+        kernels.prefill_attention(q.view(2 * 8, 2, 128)[:16], kc[:, :, :4], kc[:, :, :4], slots, 8, 0.1)
+    with pytest.raises(RuntimeError):  # head dim 64: not covered by the kernel
+        kernels.prefill_attention(q[..., :64].contiguous(), kc[..., :64].contiguous(), kc[..., :64].contiguous(),
+                                  slots, 8, 0.1)
+
+
 @pytest.mark.parametrize("t", [1, 5, 9])
 @pytest.mark.parametrize("d", [16, 512])
 def test_verify_attention_f32(cuda, t, d):
