@@ -1147,14 +1147,16 @@ static int attn_splits(int32_t keys, int32_t chunk) { return (int)((keys + chunk
 extern "C" int32_t omni_verify_attention_chunk(int32_t rows, int32_t tokens, int32_t heads,
                                                int32_t head_dim, int32_t keys) {
   (void)tokens;
-  (void)head_dim;
   if (rows <= 0 || heads <= 0 || keys <= 0) return 64;
   // About 2048 waves (8 per CU) when the rows are full, at most 8 tiles (256 keys) per split: measured on
   // config 3 (8 rows x 32 heads, 750-2400 keys), 224-256 keys per split are among the fastest and longer
-  // splits leave too few waves in flight; at least 64 keys so that a split's fixed cost stays small.
+  // splits leave too few waves in flight; at least 64 keys so that a split's fixed cost stays small.  Head dims
+  // of 256 and more run one wave per SIMD with a whole tile in registers: 256 keys per split (measured at the real
+  // checkpoint's 8 slots x 8 heads x 512: 47.7 us against 63.6 us for 96-key splits).
   const int64_t items = (int64_t)rows * heads;
   int64_t chunk = ((int64_t)keys * items + 2047) / 2048;
   chunk = (chunk + 31) / 32 * 32;
+  if (head_dim >= 256) chunk = 256;
   if (chunk > 256) chunk = 256;
   if (chunk < 64) chunk = 64;
   return (int32_t)chunk;

@@ -47,7 +47,9 @@ def test_workspace_and_split_queries():
         assert lib.omni_verify_attention_workspace(rows, t, h, d, keys, 0) == want
     # config 3: 8 rows x 32 heads, keys 2560 -> 320 keys for 2048 waves, capped at 8 tiles per split
     assert lib.omni_verify_attention_chunk(8, 5, 32, 128, 2560) == 256
-    assert lib.omni_verify_attention_chunk(8, 5, 8, 512, 2048) == 64  # the real model's 8 heads
+    # the real model's 8 heads x 512: whole-tile waves, 256 keys per split (measured fastest on MI355X)
+    assert lib.omni_verify_attention_chunk(8, 5, 8, 512, 2048) == 256
+    assert lib.omni_verify_attention_chunk(8, 5, 8, 512, 100) == 256  # one split covers every key
 
 
 FAKE = ctypes.c_void_p(0x10000)  # never dereferenced: every call below fails its checks before any launch
