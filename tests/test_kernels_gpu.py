@@ -194,6 +194,24 @@ def test_verify_attention_tickets_left_zero(cuda):
     assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
 
 
+@pytest.mark.parametrize("rows,heads", [(43, 3), (256, 1), (9, 16)])
+def test_verify_attention_halves_shapes(cuda, rows, heads):
+    """The halves kernel at unit counts it must pair exactly: an odd count (the middle workgroup takes both halves
+    of one unit), the most rows it takes (256), a count just above its threshold; ragged and empty rows.  The
+    tickets are left zero and a second call gives the same bits."""
+    g = gen(rows * 7 + heads)
+    t, d, cap = 5, 128, 1100
+    lengths = torch.randint(0, 1000, (rows,), generator=g)
+    lengths[::7] = 0
+    lengths[1::5] = torch.randint(1, 40, (len(lengths[1::5]),), generator=g)
+    keys = -(-(int(lengths.max()) + t) // 256) * 256
+    a = _attn_case(cuda, torch.bfloat16, rows, heads, d, t, cap, lengths, keys, rows + heads, BF16_TOL)
+    torch.cuda.synchronize()
+    assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
+    b = _attn_case(cuda, torch.bfloat16, rows, heads, d, t, cap, lengths, keys, rows + heads, BF16_TOL)
+    assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("split_k", [False, True])
 def test_verify_attention_graph_replays(cuda, split_k):
     """Captured in a HIP graph: every replay equals the eager result bit for bit (both decompositions)."""
