@@ -1,0 +1,239 @@
+// Causal attention over whole contexts for gfx950: the prefill's
+//     F.scaled_dot_product_attention(q, k, v, is_causal=True)
+// (src/omniasr_trt/decode.py:163-164) over the cache rows ``kernels.rope_kv`` has just written.  Query p of context
+// b attends to keys [0, p] of its cache row; fp32 accumulation, bf16 in and out, head_dim 128.
+#include <math.h>
+
+#include "attn_tiles.h"
+#include "common.h"
+
+namespace omni {
+
+// Causal attention over whole contexts (the prefill): query p of context b attends to keys [0, p] of its cache row.
+// One workgroup of kPfWaves waves per (query block, head, context), the longest blocks first.  The block's 32-key
+// tiles go through LDS once for all of its waves (double-buffered: tile t + 1's global loads are in flight during
+// tile t's math).  Each wave holds kPfSub groups of 16 queries: per tile it reads the K / V fragments from LDS and
+// builds the V operands once, then runs S^T = K Q^T, the lazy softmax (causal limit as the key limit) and
+// O += P V for every group that sees the tile.
+constexpr int kPfWaves = 4;
+constexpr int kPfSub = 2;  // 16-query groups per wave
+constexpr int kPfQueries = 16 * kPfSub * kPfWaves;
+constexpr int kPfRow = 128 * 2 + 16;  // LDS bytes per key row: 256 B of data, padded against bank conflicts
+
+struct PrefillArgs {
+  const uint16_t* q;    // [B * width, H, 128] bf16
+  const uint16_t* k;    // cache rows: element strides s_row / s_head, key rows contiguous (128 elements)
+  const uint16_t* v;
+  const int64_t* slots;  // [B] cache row of each context
+  int64_t s_row, s_head, cache_rows;
+  int width, H;
+  float scale_log2;
+  uint16_t* out;  // [B * width, H, 128] bf16
+};
+
+// The softmax step of one 16-query group for one tile: mask (key0 + j >= lim), lazy reference max, this lane's
+// 8 probabilities packed as the P operand.  (The same arithmetic as attend().)
+template <int NB>
+__device__ __forceinline__ u32x4_t softmax_tile(float (&sv)[8], float c_scale, SoftmaxState& st, f32x4_t (&o)[NB],
+                                                int g, int key0, int lim) {
+  bool over = false;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    sv[j] = key0 + j < lim ? sv[j] : -INFINITY;
+    over |= sv[j] > st.thr;
+  }
+  if (__any(over)) {
+    float mx = sv[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sv[j]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float m_new = fmaxf(st.m_ref, mx * c_scale);
+    rescale<NB>(st.m_ref, m_new == -INFINITY ? 0.f : m_new, st.l_run, o, g);
+    st.m_ref = m_new;
+    st.thr = m_new == -INFINITY ? -INFINITY : (m_new + kLazyLog2) / c_scale;
+  }
+  const float m_use = st.m_ref == -INFINITY ? 0.f : st.m_ref;
+  float p[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], c_scale, -m_use));
+    st.l_run += p[j];
+  }
+  u32x4_t pop;
+#pragma unroll
+  for (int w = 0; w < 4; ++w)
+    pop[w] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{p[2 * w], p[2 * w + 1]}), bf16x2_t));
+  return pop;
+}
+
+__global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attn_kernel(
+    PrefillArgs a) {
+  constexpr int D = 128, KS = D / 32;
+  __shared__ __attribute__((aligned(16))) char lds[2][2][32 * kPfRow];  // [buffer][K, V][key rows]
+  const int nqb = (a.width + kPfQueries - 1) / kPfQueries;
+  const int qb = (nqb - 1 - (int)blockIdx.x) * kPfQueries;  // the longest blocks first
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t slot = clamp64(a.slots[b], 0, a.cache_rows - 1);
+  const uint16_t* kbase = a.k + slot * a.s_row + h * a.s_head;
+  const uint16_t* vbase = a.v + slot * a.s_row + h * a.s_head;
+  const int kend = min(qb + kPfQueries, a.width);  // keys the block's last query sees
+  const int nt = (kend + 31) >> 5;
+
+  // Global -> LDS: thread tid moves 16-byte chunks tid and tid + 256 of the tile's K and of its V (32 rows x 256 B
+  // each).  Rows past the context read its last key (finite: masked by the causal limit, never NaN).
+  u32x4_t stage[4];
+  auto fetch = [&](int t) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int ci = tid + e * 256, r = ci >> 4, col = ci & 15;
+      const int key = min(t * 32 + r, a.width - 1);
+      stage[e] = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)key * D + col * 8);
+      stage[2 + e] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)key * D + col * 8);
+    }
+  };
+  auto put = [&](int buf) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int ci = tid + e * 256, r = ci >> 4, col = ci & 15;
+      *reinterpret_cast<u32x4_t*>(&lds[buf][0][r * kPfRow + col * 16]) = stage[e];
+      *reinterpret_cast<u32x4_t*>(&lds[buf][1][r * kPfRow + col * 16]) = stage[2 + e];
+    }
+  };
+
+  // The wave's groups: queries q0[u] + c, u < kPfSub (group u of wave w: block rows 16 (w + kPfWaves u)).
+  int q0[kPfSub];
+  u32x4_t qop[kPfSub][KS];  // B operand of S^T = K Q^T: lane (c, g) holds q[q0 + c][32s + 8g .. +7] (0 past the end)
+  SoftmaxState st[kPfSub];
+  f32x4_t o[kPfSub][D / 16];
+#pragma unroll
+  for (int u = 0; u < kPfSub; ++u) {
+    q0[u] = qb + 16 * (w + kPfWaves * u);
+    const bool live = q0[u] + c < a.width;
+    const uint16_t* qrow = a.q + ((int64_t)(b * a.width + (live ? q0[u] + c : 0)) * a.H + h) * D + g * 8;
+#pragma unroll
+    for (int s2 = 0; s2 < KS; ++s2)
+      qop[u][s2] = live ? *reinterpret_cast<const u32x4_t*>(qrow + s2 * 32) : u32x4_t{0u, 0u, 0u, 0u};
+    st[u] = SoftmaxState{-INFINITY, -INFINITY, 0.f};
+#pragma unroll
+    for (int nb = 0; nb < D / 16; ++nb) o[u][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  fetch(0);
+  put(0);
+  __syncthreads();
+  for (int t = 0; t < nt; ++t) {
+    fetch(t + 1 < nt ? t + 1 : t);  // unconditional: the last iteration re-reads its own tile (cache hit)
+    // Groups that see the tile (wave-uniform): a live group whose last query reaches the tile's first key.
+    bool act[kPfSub];
+    bool any = false;
+#pragma unroll
+    for (int u = 0; u < kPfSub; ++u) {
+      act[u] = q0[u] < a.width && t * 32 <= q0[u] + 15;
+      any |= act[u];
+    }
+    if (any) {
+      const char* kl = lds[t & 1][0];
+      const char* vl = lds[t & 1][1];
+      u32x4_t pop[kPfSub];
+      {
+        u32x4_t kf[2][KS];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          const int rk = 8 * (c >> 2) + 4 * mb + (c & 3);
+#pragma unroll
+          for (int s2 = 0; s2 < KS; ++s2) kf[mb][s2] = *reinterpret_cast<const u32x4_t*>(kl + rk * kPfRow + g * 16 + s2 * 64);
+        }
+#pragma unroll
+        for (int u = 0; u < kPfSub; ++u) {
+          if (!act[u]) continue;
+          f32x4_t sacc[2];
+#pragma unroll
+          for (int mb = 0; mb < 2; ++mb) {
+            sacc[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s2 = 0; s2 < KS; ++s2)
+              sacc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[mb][s2]),
+                                                                 __builtin_bit_cast(bf16x8_t, qop[u][s2]), sacc[mb],
+                                                                 0, 0, 0);
+          }
+          float sv[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) sv[j] = sacc[j >> 2][j & 3];
+          pop[u] = softmax_tile<D / 16>(sv, a.scale_log2, st[u], o[u], g, t * 32 + 8 * g, q0[u] + c + 1);
+        }
+      }
+      u32x4_t vf[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) vf[j] = *reinterpret_cast<const u32x4_t*>(vl + (8 * g + j) * kPfRow + c * 16);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        u32x4_t bop;
+#pragma unroll
+        for (int w2 = 0; w2 < 4; ++w2)
+          bop[w2] = __builtin_amdgcn_perm(vf[2 * w2 + 1][e >> 1], vf[2 * w2][e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
+#pragma unroll
+        for (int u = 0; u < kPfSub; ++u) {
+          if (!act[u]) continue;
+          o[u][e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pop[u]),
+                                                            __builtin_bit_cast(bf16x8_t, bop), o[u][e], 0, 0, 0);
+        }
+      }
+    }
+    put((t + 1) & 1);
+    __syncthreads();
+  }
+
+  // ---- each group's 16 output rows: O / l, rounded to bf16
+#pragma unroll
+  for (int u = 0; u < kPfSub; ++u) {
+    float l_tot = st[u].l_run + __shfl_xor(st[u].l_run, 16, kWave);
+    l_tot += __shfl_xor(l_tot, 32, kWave);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float li = __shfl(l_tot, 4 * g + i, kWave);
+      const int qq = q0[u] + 4 * g + i;
+      if (qq >= a.width) continue;
+      const float div = li > 0.f ? li : 1.f;
+      u32x4_t wv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wv[e] = pack_bf16x2(o[u][2 * e][i] / div, o[u][2 * e + 1][i] / div);
+      *reinterpret_cast<u32x4_t*>(a.out + ((int64_t)(b * a.width + qq) * a.H + h) * D + c * 8) = wv;
+    }
+  }
+}
+
+}  // namespace omni
+
+extern "C" int omni_prefill_attention(const void* q, const void* k_cache, const void* v_cache, int64_t stride_row,
+                                      int64_t stride_head, int64_t stride_pos, int64_t cache_len,
+                                      int64_t cache_rows, const int64_t* slots, int32_t contexts, int32_t width,
+                                      int32_t heads, int32_t head_dim, float scale, void* out, int32_t dtype,
+                                      void* stream) {
+  if (contexts < 0 || width < 0 || heads <= 0 || cache_rows <= 0) return OMNI_ERR_INVALID;
+  if (dtype != OMNI_BF16) return OMNI_ERR_DTYPE;
+  if (head_dim != 128 || stride_pos != head_dim) return OMNI_ERR_SHAPE;
+  if (!(scale > 0.f) || width > cache_len) return OMNI_ERR_INVALID;
+  if (contexts == 0 || width == 0) return OMNI_OK;
+  if (!q || !k_cache || !v_cache || !slots || !out) return OMNI_ERR_INVALID;
+  if (((uintptr_t)q | (uintptr_t)out | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15u) return OMNI_ERR_INVALID;
+  if ((stride_row | stride_head) % 8 != 0) return OMNI_ERR_INVALID;
+  if ((int64_t)contexts * width * heads >= (int64_t{1} << 31) / 128) return OMNI_ERR_INVALID;
+  omni::PrefillArgs a;
+  a.q = (const uint16_t*)q;
+  a.k = (const uint16_t*)k_cache;
+  a.v = (const uint16_t*)v_cache;
+  a.slots = slots;
+  a.s_row = stride_row;
+  a.s_head = stride_head;
+  a.cache_rows = cache_rows;
+  a.width = width;
+  a.H = heads;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.out = (uint16_t*)out;
+  dim3 grid((width + omni::kPfQueries - 1) / omni::kPfQueries, heads, contexts);
+  omni::prefill_attn_kernel<<<grid, 64 * omni::kPfWaves, 0, (hipStream_t)stream>>>(a);
+  return omni_launch_status();
+}

@@ -7,33 +7,27 @@
 // log-sum-exp with w_s = exp(m_s - max m) (0 for an empty split) and out = sum w_s acc_s /
 // sum w_s l_s (0 when that sum is 0).
 //
-// Work decompositions.  The unit of work is a (head, row) pair; one wave serves all of the row's T <= 16 queries
-// with a single read of K and V, 32 keys at a time.
-//  * Halves (bf16, head_dim 128, T <= 14, rows x heads >= 128; verify_attn_pair_kernel): one 8-wave workgroup
-//    per CU-sized share, each taking the first half of a long unit and the second half of a short one (units
-//    ranked by length on the device), so every CU streams about the same number of tiles -- a CU reads at most
-//    ~30 GB/s, so HBM runs at full rate only while nearly all CUs are busy.  The 8 waves interleave a half's tiles
-//    and merge in LDS; the second half of a unit to finish merges the two halves (partials written through to the
-//    coherence point, atomic ticket per unit).  One launch, no partials in HBM beyond 2 x T x D per unit.
+// Work decompositions.  The unit of work is a (head, row) pair; its T <= 16 queries share one read of K and V,
+// 32 keys at a time (the tile math of attn_tiles.h).
+//  * Halves (bf16, head_dim 128, T <= 11, rows <= 256, rows x heads >= 128; verify_attn_pair_kernel): one 8-wave
+//    workgroup per unit, taking the first half of a long unit and the second half of a short one (units ranked by
+//    length on the device), so every CU streams about the same number of tiles -- a CU reads at most ~30 GB/s, so
+//    HBM runs at full rate only while nearly all CUs are busy.  The waves' tiles run through both halves in one
+//    pipeline; a unit's two halves meet through partials written through to the coherence point and a ticket per
+//    unit, and the workgroup of the second half fetches the first while its waves finish.  One launch; results
+//    do not depend on timing.
 //  * Split-K (every other shape; verify_attn_mfma_kernel / verify_attn_valu_kernel): one wavefront per (key
 //    split, head, row), grid (splits, heads, rows).  A row's 32-key tiles are dealt round-robin over its splits.
 //    Splits beyond a row's last key exit at once, so the grid depends on the key bucket only (graph capture)
 //    while ragged rows read just their own keys.  The splits' partials are merged by a second launch or by the
 //    last split to finish (ticket per (row, head)); a row with one split writes its output directly.
-// bf16, head_dim a multiple of 128: both products run on v_mfma_f32_16x16x32_bf16 with the T
-// queries padded to the 16-wide MFMA dimension, and every K/V element is loaded straight into the
-// MFMA operand layout with 128-bit loads (no LDS):
-//   S^T = K Q^T  -- A = K (16 keys x 32 dims), B = Q^T.  Lane (c = lane%16, g = lane/16) loads
-//                   key kb + 8*(c/4) + 4*mb + c%4 (mb = 0, 1) so that the output of the two MFMAs
-//                   leaves lane (c, g) the scores of query c for keys kb + 8g .. kb + 8g + 7;
-//   O  = P V     -- A = P (those 8 scores, rounded to bf16, are exactly lane (c, g)'s A operand),
-//                   B = V (32 keys x 16 dims).  Output column c of block (gg, e) is dimension
-//                   128*gg + 8c + e, so lane (c, g) loads 8 consecutive dimensions of 8 keys
-//                   (8 x 16 bytes) and transposes them in registers into the 8 B operands.
-// fp32, or bf16 with another head_dim: a vector-ALU wave with fp32 products (the reference's
-// IEEE path for fp32 agreement checks).
+// bf16 with head_dim a multiple of 128 runs on MFMA with every K/V element loaded straight into the operand layout
+// (128-bit loads, no LDS); fp32, or bf16 with another head_dim, runs a vector-ALU wave with fp32 products (the
+// reference's IEEE path for fp32 agreement checks).  The beams' attention (context by these kernels, generated
+// keys through pointers) is at the end of the file.
 #include <math.h>
 
+#include "attn_tiles.h"
 #include "common.h"
 
 namespace omni {
@@ -269,152 +263,6 @@ __device__ __forceinline__ void finish_split(const AttnArgs& a, int b, int h, in
 }
 
 // ---------------------------------------------------------------------------------------------- MFMA
-
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-// Scores are kept relative to a reference max m_ref (log2 domain) that only moves when a score exceeds it by
-// more than 2^kLazyLog2: the cross-lane max and the rescale of O are skipped for almost every tile, and
-// probabilities stay <= 2^kLazyLog2 (exact in fp32, and bf16 keeps its relative precision at any scale).
-constexpr float kLazyLog2 = 8.0f;
-
-// One 32-key tile of K and V in MFMA operand layout (see the file comment).
-template <int D>
-struct KVTile {
-  static constexpr int KS = D / 32, NG = D / 128;
-  u32x4_t k[2][KS];
-  u32x4_t v[NG][8];
-};
-
-__device__ __forceinline__ u32x4_t ld16(const char* p) { return *reinterpret_cast<const u32x4_t*>(p); }
-
-// One 32-key tile of K and V into MFMA operand layout.  Key rows are contiguous (D elements apart), so each load is
-// the wave-uniform tile base plus a 32-bit lane offset.  K rows past ``kmax`` (the last cache position, relative to
-// the tile's first key; 31 inside the cache) are read at kmax; their scores are masked.  V rows at or past
-// ``vstop`` (the end of the keys in use, relative; 32 for a full tile, >= 1 for a tile that is attended) are read
-// at vstop - 1, a key in use: every query's probability of those keys is 0, and 0 times a finite value of a key in
-// use adds nothing (stale memory past the keys could hold NaN).  Only addresses are clamped, never loaded data, so
-// nothing waits for a tile's loads before its math.
-template <int D>
-__device__ __forceinline__ void load_tile_clamped(KVTile<D>& t, const char* kt, const char* vt, int kmax, int vstop,
-                                                  int c, int g) {
-  constexpr uint32_t kRow = D * 2;
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
-    int rk = 8 * (c >> 2) + 4 * mb + (c & 3);
-    rk = rk < kmax ? rk : kmax;
-    const uint32_t ko = (uint32_t)rk * kRow + g * 16;
-#pragma unroll
-    for (int s = 0; s < KVTile<D>::KS; ++s) t.k[mb][s] = ld16(kt + ko + s * 64);
-  }
-  int vmax = vstop - 1 < kmax ? vstop - 1 : kmax;
-  vmax = vmax > 0 ? vmax : 0;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int rv = 8 * g + j;
-    const uint32_t vo = (uint32_t)(rv < vmax ? rv : vmax) * kRow + c * 16;
-#pragma unroll
-    for (int gg = 0; gg < KVTile<D>::NG; ++gg) t.v[gg][j] = ld16(vt + vo + gg * 256);
-  }
-}
-
-// S^T for the tile: lane (c, g) gets query c's raw scores for keys kb + 8g + j, j = 0..7.
-template <int D>
-__device__ __forceinline__ void tile_scores(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float (&sv)[8]) {
-  f32x4_t sacc[2];
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
-    sacc[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < D / 32; ++s)
-      sacc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, t.k[mb][s]),
-                                                         __builtin_bit_cast(bf16x8_t, qop[s]), sacc[mb], 0, 0, 0);
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) sv[j] = sacc[j >> 2][j & 3];
-}
-
-// Move the reference max of every row to ``m_new`` (rows 4g + i of O live in this lane; their alphas in lanes
-// 4g + i), rescaling O and this lane's share of the probability sum.
-template <int NB>
-__device__ __forceinline__ void rescale(float m_old, float m_new_use, float& l_run, f32x4_t (&o)[NB], int g) {
-  const float alpha = __builtin_amdgcn_exp2f(m_old - m_new_use);  // m_old = -inf: 0
-  l_run *= alpha;
-  float al[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * g + i, kWave);
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[nb][i] *= al[i];
-  }
-}
-
-// O += P V for the tile: P from this lane's 8 probabilities (its A operand), V transposed in registers.
-template <int D>
-__device__ __forceinline__ void tile_pv(const KVTile<D>& t, const float (&p)[8], f32x4_t (&o)[D / 16]) {
-  u32x4_t pop;
-#pragma unroll
-  for (int w = 0; w < 4; ++w)
-    pop[w] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{p[2 * w], p[2 * w + 1]}), bf16x2_t));
-#pragma unroll
-  for (int gg = 0; gg < D / 128; ++gg) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      u32x4_t bop;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t lo = t.v[gg][2 * w][e >> 1];
-        const uint32_t hi = t.v[gg][2 * w + 1][e >> 1];
-        // element e of rows 2w and 2w+1: one byte permute
-        bop[w] = __builtin_amdgcn_perm(hi, lo, (e & 1) ? 0x07060302u : 0x05040100u);
-      }
-      o[gg * 8 + e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pop),
-                                                              __builtin_bit_cast(bf16x8_t, bop), o[gg * 8 + e], 0,
-                                                              0, 0);
-    }
-  }
-}
-
-struct SoftmaxState {
-  float m_ref;  // reference max of query c (log2 domain), equal over g
-  float thr;    // raw-score threshold above which m_ref must move
-  float l_run;  // this lane's share of query c's probability sum (relative to m_ref)
-};
-
-// One tile: scores, the causal / end-of-row mask (key0 + j >= lim: query c does not see key j of this lane), the
-// lazy reference max, probabilities, O += P V.  The mask is a no-op on tiles every query sees whole.
-template <int D>
-__device__ __forceinline__ void attend(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float c_scale,
-                                       SoftmaxState& st, f32x4_t (&o)[D / 16], int g, int key0, int lim) {
-  float sv[8];
-  tile_scores<D>(t, qop, sv);
-  bool over = false;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    sv[j] = key0 + j < lim ? sv[j] : -INFINITY;
-    over |= sv[j] > st.thr;
-  }
-  if (__any(over)) {
-    float mx = sv[0];
-#pragma unroll
-    for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sv[j]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(st.m_ref, mx * c_scale);
-    rescale<D / 16>(st.m_ref, m_new == -INFINITY ? 0.f : m_new, st.l_run, o, g);
-    st.m_ref = m_new;
-    st.thr = m_new == -INFINITY ? -INFINITY : (m_new + kLazyLog2) / c_scale;
-  }
-  const float m_use = st.m_ref == -INFINITY ? 0.f : st.m_ref;  // no key seen yet: every probability is 0
-  float p[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], c_scale, -m_use));
-    st.l_run += p[j];
-  }
-  tile_pv<D>(t, p, o);
-}
 
 // One split's share of row b, head h: tiles sp, sp + nact, sp + 2 nact, ... of the row (r.nact splits).  Leaves
 // the split's unnormalised output rows in ``o`` and its softmax state in ``st``.
@@ -1600,237 +1448,4 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
     return omni_launch_status();
   }
   return launch_combine(a, groups, dtype, s);
-}
-
-// ---------------------------------------------------------------------------------------------- prefill (causal)
-
-namespace omni {
-
-// Causal attention over whole contexts (the prefill): query p of context b attends to keys [0, p] of its cache row.
-// One workgroup of kPfWaves waves per (query block, head, context), the longest blocks first.  The block's 32-key
-// tiles go through LDS once for all of its waves (double-buffered: tile t + 1's global loads are in flight during
-// tile t's math).  Each wave holds kPfSub groups of 16 queries: per tile it reads the K / V fragments from LDS and
-// builds the V operands once, then runs S^T = K Q^T, the lazy softmax (causal limit as the key limit) and
-// O += P V for every group that sees the tile.
-constexpr int kPfWaves = 4;
-constexpr int kPfSub = 2;  // 16-query groups per wave
-constexpr int kPfQueries = 16 * kPfSub * kPfWaves;
-constexpr int kPfRow = 128 * 2 + 16;  // LDS bytes per key row: 256 B of data, padded against bank conflicts
-
-struct PrefillArgs {
-  const uint16_t* q;    // [B * width, H, 128] bf16
-  const uint16_t* k;    // cache rows: element strides s_row / s_head, key rows contiguous (128 elements)
-  const uint16_t* v;
-  const int64_t* slots;  // [B] cache row of each context
-  int64_t s_row, s_head, cache_rows;
-  int width, H;
-  float scale_log2;
-  uint16_t* out;  // [B * width, H, 128] bf16
-};
-
-// The softmax step of one 16-query group for one tile: mask (key0 + j >= lim), lazy reference max, this lane's
-// 8 probabilities packed as the P operand.  (The same arithmetic as attend().)
-template <int NB>
-__device__ __forceinline__ u32x4_t softmax_tile(float (&sv)[8], float c_scale, SoftmaxState& st, f32x4_t (&o)[NB],
-                                                int g, int key0, int lim) {
-  bool over = false;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    sv[j] = key0 + j < lim ? sv[j] : -INFINITY;
-    over |= sv[j] > st.thr;
-  }
-  if (__any(over)) {
-    float mx = sv[0];
-#pragma unroll
-    for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sv[j]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(st.m_ref, mx * c_scale);
-    rescale<NB>(st.m_ref, m_new == -INFINITY ? 0.f : m_new, st.l_run, o, g);
-    st.m_ref = m_new;
-    st.thr = m_new == -INFINITY ? -INFINITY : (m_new + kLazyLog2) / c_scale;
-  }
-  const float m_use = st.m_ref == -INFINITY ? 0.f : st.m_ref;
-  float p[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], c_scale, -m_use));
-    st.l_run += p[j];
-  }
-  u32x4_t pop;
-#pragma unroll
-  for (int w = 0; w < 4; ++w)
-    pop[w] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{p[2 * w], p[2 * w + 1]}), bf16x2_t));
-  return pop;
-}
-
-__global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attn_kernel(
-    PrefillArgs a) {
-  constexpr int D = 128, KS = D / 32;
-  __shared__ __attribute__((aligned(16))) char lds[2][2][32 * kPfRow];  // [buffer][K, V][key rows]
-  const int nqb = (a.width + kPfQueries - 1) / kPfQueries;
-  const int qb = (nqb - 1 - (int)blockIdx.x) * kPfQueries;  // the longest blocks first
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t slot = clamp64(a.slots[b], 0, a.cache_rows - 1);
-  const uint16_t* kbase = a.k + slot * a.s_row + h * a.s_head;
-  const uint16_t* vbase = a.v + slot * a.s_row + h * a.s_head;
-  const int kend = min(qb + kPfQueries, a.width);  // keys the block's last query sees
-  const int nt = (kend + 31) >> 5;
-
-  // Global -> LDS: thread tid moves 16-byte chunks tid and tid + 256 of the tile's K and of its V (32 rows x 256 B
-  // each).  Rows past the context read its last key (finite: masked by the causal limit, never NaN).
-  u32x4_t stage[4];
-  auto fetch = [&](int t) {
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int ci = tid + e * 256, r = ci >> 4, col = ci & 15;
-      const int key = min(t * 32 + r, a.width - 1);
-      stage[e] = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)key * D + col * 8);
-      stage[2 + e] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)key * D + col * 8);
-    }
-  };
-  auto put = [&](int buf) {
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int ci = tid + e * 256, r = ci >> 4, col = ci & 15;
-      *reinterpret_cast<u32x4_t*>(&lds[buf][0][r * kPfRow + col * 16]) = stage[e];
-      *reinterpret_cast<u32x4_t*>(&lds[buf][1][r * kPfRow + col * 16]) = stage[2 + e];
-    }
-  };
-
-  // The wave's groups: queries q0[u] + c, u < kPfSub (group u of wave w: block rows 16 (w + kPfWaves u)).
-  int q0[kPfSub];
-  u32x4_t qop[kPfSub][KS];  // B operand of S^T = K Q^T: lane (c, g) holds q[q0 + c][32s + 8g .. +7] (0 past the end)
-  SoftmaxState st[kPfSub];
-  f32x4_t o[kPfSub][D / 16];
-#pragma unroll
-  for (int u = 0; u < kPfSub; ++u) {
-    q0[u] = qb + 16 * (w + kPfWaves * u);
-    const bool live = q0[u] + c < a.width;
-    const uint16_t* qrow = a.q + ((int64_t)(b * a.width + (live ? q0[u] + c : 0)) * a.H + h) * D + g * 8;
-#pragma unroll
-    for (int s2 = 0; s2 < KS; ++s2)
-      qop[u][s2] = live ? *reinterpret_cast<const u32x4_t*>(qrow + s2 * 32) : u32x4_t{0u, 0u, 0u, 0u};
-    st[u] = SoftmaxState{-INFINITY, -INFINITY, 0.f};
-#pragma unroll
-    for (int nb = 0; nb < D / 16; ++nb) o[u][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
-
-  fetch(0);
-  put(0);
-  __syncthreads();
-  for (int t = 0; t < nt; ++t) {
-    fetch(t + 1 < nt ? t + 1 : t);  // unconditional: the last iteration re-reads its own tile (cache hit)
-    // Groups that see the tile (wave-uniform): a live group whose last query reaches the tile's first key.
-    bool act[kPfSub];
-    bool any = false;
-#pragma unroll
-    for (int u = 0; u < kPfSub; ++u) {
-      act[u] = q0[u] < a.width && t * 32 <= q0[u] + 15;
-      any |= act[u];
-    }
-    if (any) {
-      const char* kl = lds[t & 1][0];
-      const char* vl = lds[t & 1][1];
-      u32x4_t pop[kPfSub];
-      {
-        u32x4_t kf[2][KS];
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-          const int rk = 8 * (c >> 2) + 4 * mb + (c & 3);
-#pragma unroll
-          for (int s2 = 0; s2 < KS; ++s2) kf[mb][s2] = *reinterpret_cast<const u32x4_t*>(kl + rk * kPfRow + g * 16 + s2 * 64);
-        }
-#pragma unroll
-        for (int u = 0; u < kPfSub; ++u) {
-          if (!act[u]) continue;
-          f32x4_t sacc[2];
-#pragma unroll
-          for (int mb = 0; mb < 2; ++mb) {
-            sacc[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s2 = 0; s2 < KS; ++s2)
-              sacc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[mb][s2]),
-                                                                 __builtin_bit_cast(bf16x8_t, qop[u][s2]), sacc[mb],
-                                                                 0, 0, 0);
-          }
-          float sv[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) sv[j] = sacc[j >> 2][j & 3];
-          pop[u] = softmax_tile<D / 16>(sv, a.scale_log2, st[u], o[u], g, t * 32 + 8 * g, q0[u] + c + 1);
-        }
-      }
-      u32x4_t vf[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) vf[j] = *reinterpret_cast<const u32x4_t*>(vl + (8 * g + j) * kPfRow + c * 16);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        u32x4_t bop;
-#pragma unroll
-        for (int w2 = 0; w2 < 4; ++w2)
-          bop[w2] = __builtin_amdgcn_perm(vf[2 * w2 + 1][e >> 1], vf[2 * w2][e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
-#pragma unroll
-        for (int u = 0; u < kPfSub; ++u) {
-          if (!act[u]) continue;
-          o[u][e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pop[u]),
-                                                            __builtin_bit_cast(bf16x8_t, bop), o[u][e], 0, 0, 0);
-        }
-      }
-    }
-    put((t + 1) & 1);
-    __syncthreads();
-  }
-
-  // ---- each group's 16 output rows: O / l, rounded to bf16
-#pragma unroll
-  for (int u = 0; u < kPfSub; ++u) {
-    float l_tot = st[u].l_run + __shfl_xor(st[u].l_run, 16, kWave);
-    l_tot += __shfl_xor(l_tot, 32, kWave);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float li = __shfl(l_tot, 4 * g + i, kWave);
-      const int qq = q0[u] + 4 * g + i;
-      if (qq >= a.width) continue;
-      const float div = li > 0.f ? li : 1.f;
-      u32x4_t wv;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) wv[e] = pack_bf16x2(o[u][2 * e][i] / div, o[u][2 * e + 1][i] / div);
-      *reinterpret_cast<u32x4_t*>(a.out + ((int64_t)(b * a.width + qq) * a.H + h) * D + c * 8) = wv;
-    }
-  }
-}
-
-}  // namespace omni
-
-extern "C" int omni_prefill_attention(const void* q, const void* k_cache, const void* v_cache, int64_t stride_row,
-                                      int64_t stride_head, int64_t stride_pos, int64_t cache_len,
-                                      int64_t cache_rows, const int64_t* slots, int32_t contexts, int32_t width,
-                                      int32_t heads, int32_t head_dim, float scale, void* out, int32_t dtype,
-                                      void* stream) {
-  if (contexts < 0 || width < 0 || heads <= 0 || cache_rows <= 0) return OMNI_ERR_INVALID;
-  if (dtype != OMNI_BF16) return OMNI_ERR_DTYPE;
-  if (head_dim != 128 || stride_pos != head_dim) return OMNI_ERR_SHAPE;
-  if (!(scale > 0.f) || width > cache_len) return OMNI_ERR_INVALID;
-  if (contexts == 0 || width == 0) return OMNI_OK;
-  if (!q || !k_cache || !v_cache || !slots || !out) return OMNI_ERR_INVALID;
-  if (!attention_aligned(q, out, k_cache, v_cache, stride_row, stride_head, stride_pos, head_dim, dtype))
-    return OMNI_ERR_INVALID;
-  if ((int64_t)contexts * width * heads >= (int64_t{1} << 31) / 128) return OMNI_ERR_INVALID;
-  omni::PrefillArgs a;
-  a.q = (const uint16_t*)q;
-  a.k = (const uint16_t*)k_cache;
-  a.v = (const uint16_t*)v_cache;
-  a.slots = slots;
-  a.s_row = stride_row;
-  a.s_head = stride_head;
-  a.cache_rows = cache_rows;
-  a.width = width;
-  a.H = heads;
-  a.scale_log2 = scale * 1.4426950408889634f;
-  a.out = (uint16_t*)out;
-  dim3 grid((width + omni::kPfQueries - 1) / omni::kPfQueries, heads, contexts);
-  omni::prefill_attn_kernel<<<grid, 64 * omni::kPfWaves, 0, (hipStream_t)stream>>>(a);
-  return omni_launch_status();
 }
