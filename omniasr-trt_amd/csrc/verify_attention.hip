@@ -100,20 +100,10 @@ __device__ __forceinline__ void put_partial(float* p, float v, bool through) {
   else *p = v;
 }
 
-// Four floats written through to the coherence point in one 16-byte store (agent scope: the cache-policy bit the
-// compiler sets on agent-scope atomic stores).  Only waited for by an explicit s_waitcnt.
-__device__ __forceinline__ void put_through4(float* p, f32x4_t v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
-}
-
 // Two floats (m, l) written through in one 8-byte agent-scope store.
 __device__ __forceinline__ void put_through2(float* p, float x, float y) {
   const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
   __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float get_through(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Partial slot of the q-th partial to merge: the row's key splits, then the generated-keys slot if any.
@@ -121,15 +111,15 @@ __device__ __forceinline__ int merge_slot(const AttnArgs& a, int nact, int q) {
   return q < nact ? q : a.gen_split;
 }
 
-// Log-sum-exp merge of the partials of (row b, head h) by one wave; writes the output.  THROUGH: the partials are
-// read at the coherence point (in-kernel merge).
-template <typename OutT, bool THROUGH>
+// Log-sum-exp merge of the partials of (row b, head h) by one wave (the merge launch, after the split kernel);
+// writes the output.
+template <typename OutT>
 __device__ void merge_splits(const AttnArgs& a, int b, int h, int nact) {
   const int lane = lane_id();
   const int nq = nact + (a.gen_split >= 0 ? 1 : 0);
   const int64_t split0 = ((int64_t)b * a.H + h) * a.splits;
   OutT* out = reinterpret_cast<OutT*>(a.out);
-  auto get = [](const float* p) { return THROUGH ? get_through(p) : *p; };
+  auto get = [](const float* p) { return *p; };
   for (int t = 0; t < a.T; ++t) {
     float top = -INFINITY;
     for (int q = lane; q < nq; q += kWave)
@@ -151,14 +141,7 @@ __device__ void merge_splits(const AttnArgs& a, int b, int h, int nact) {
         const int64_t slot = (split0 + merge_slot(a, nact, q)) * a.T + t;
         const float m = get(a.part_ml + slot * 2);
         const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - top);
-        const float* src = a.part_o + slot * a.D + d;
-        f32x4_t po;
-        if constexpr (THROUGH) {
-          po = f32x4_t{get_through(src), get_through(src + 1), get_through(src + 2), get_through(src + 3)};
-        } else {
-          po = *reinterpret_cast<const f32x4_t*>(src);
-        }
-        acc += w * po;
+        acc += w * *reinterpret_cast<const f32x4_t*>(a.part_o + slot * a.D + d);
       }
       store4<OutT>(orow + d, acc / div);
     }
@@ -940,7 +923,7 @@ __global__ __launch_bounds__(64) void verify_attn_combine_kernel(AttnArgs a) {
   const int64_t split0 = ((int64_t)b * a.H + h) * a.splits;
   OutT* orow = reinterpret_cast<OutT*>(a.out) + ((int64_t)(b * T + t) * a.H + h) * D;
   if (nq > kCombineMaxSplits) {  // beyond the unrolled case: the generic merge
-    if (t == 0) merge_splits<OutT, false>(a, b, h, nact);
+    if (t == 0) merge_splits<OutT>(a, b, h, nact);
     return;
   }
   const int d0 = lane * DPL;
