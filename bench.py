@@ -359,14 +359,17 @@ def beam_leg(pkg, torch, w: Workload, steps: int, warmup: int, reps: int) -> dic
 
 class AttentionCaches:
     """Config 3 without the decoder: 12 disjoint bf16 K/V sets [8, 32, 2560, 128] (2.5 GB touched per cycle: the
-    256 MB Infinity Cache cannot serve them) standing in for the 12 layers' caches."""
+    256 MB Infinity Cache cannot serve them) standing in for the 12 layers' caches; ``heads`` / ``dim`` 8 / 512 give
+    the real checkpoint's shape."""
 
-    def __init__(self, torch, layers: int = 12, cap: int = 2560, seed: int = 1005):
+    def __init__(self, torch, layers: int = 12, cap: int = 2560, seed: int = 1005, heads: int = 32, dim: int = 128):
         g = torch.Generator(device="cuda").manual_seed(seed)
-        self.k = [torch.randn(SLOTS, 32, cap, 128, device="cuda", generator=g).to(torch.bfloat16) for _ in range(layers)]
-        self.v = [torch.randn(SLOTS, 32, cap, 128, device="cuda", generator=g).to(torch.bfloat16) for _ in range(layers)]
+        self.k = [torch.randn(SLOTS, heads, cap, dim, device="cuda", generator=g).to(torch.bfloat16)
+                  for _ in range(layers)]
+        self.v = [torch.randn(SLOTS, heads, cap, dim, device="cuda", generator=g).to(torch.bfloat16)
+                  for _ in range(layers)]
         self.layers = [None] * layers
-        self.heads, self.head_dim, self.capacity = 32, 128, cap
+        self.heads, self.head_dim, self.capacity = heads, dim, cap
 
 
 def copy_reference(torch, nbytes: int = 256 << 20, reps: int = 4) -> dict:
@@ -528,6 +531,10 @@ def main() -> int:
         print(f"[bench] verify attention T=5: {attn['us']} us, {attn['GBps']} GB/s", file=sys.stderr, flush=True)
         sweep = [time_attention(pkg, torch, w.dec, t, args.attn_reps) for t in (1, 3, 9)] if not args.no_extra else []
         extra = time_small_kernels(pkg, torch, w.dec) if not args.no_extra else {}
+        if not args.no_extra:  # the real checkpoint's attention shape: 8 heads x 512 (split-K + merge launch)
+            real = AttentionCaches(torch, heads=8, dim=512)
+            extra["verify_attention_real_8x8x512"] = time_attention(pkg, torch, real, DRAFT + 1, args.attn_reps)
+            del real
         cpu = None
         if not args.no_cpu:
             print(f"[bench] CPU baseline ({args.cpu_seconds:.0f} s)", file=sys.stderr, flush=True)
