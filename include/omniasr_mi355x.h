@@ -218,7 +218,7 @@ int omni_accept(const int64_t *tokens, const int64_t *nxt, int32_t *out, int64_t
                 int64_t limit, int64_t eos, void *stream);
 
 /*
- * Verify logits -> greedy argmax -> acceptance, in one launch.  Replaces
+ * Verify logits -> greedy argmax -> acceptance.  Replaces
  * ``F.log_softmax(logits, -1).argmax(-1)`` of the drafted step (src/omniasr_trt/spec.py:106-107)
  * and of the one-token step (src/omniasr_trt/decode.py:218-224), followed by omni_accept.
  *
@@ -227,7 +227,9 @@ int omni_accept(const int64_t *tokens, const int64_t *nxt, int32_t *out, int64_t
  * ((x_i - max) - log(sum_j exp(x_j - max)) in fp32, then rounded to the logits' type), reaches its
  * maximum.  It is written to nxt[r] (int64) when ``nxt`` is not NULL, then every row is accepted as
  * by omni_accept.  ``start``, ``use_draft`` and ``draft_next`` may be NULL together (the one-token
- * step).  T: 1..64.
+ * step).  T: 1..64.  With ``nxt`` and a vocabulary up to 32768 bf16 / 16384 fp32 entries, two
+ * launches (an argmax workgroup per row, then the acceptance); otherwise one (a workgroup per slot),
+ * for vocabularies up to 131072 bf16 / 65536 fp32 entries.
  */
 int omni_greedy_accept(const void *logits, int64_t logits_stride, int32_t vocab,
                        int32_t logits_dtype, const int64_t *tokens, int64_t *nxt, int32_t *out,

@@ -10,11 +10,12 @@
 //
 // accept: ``_accept`` (src/omniasr_trt/kernels.py:271-291).
 //
-// Layout: one 1024-thread workgroup per slot reads all T logit rows of the slot (T*V*2 bytes,
-// 100 KB at T = 5, V = 10288) with 128-bit loads issued together, reduces max, sum and the first
-// index per row through wave shuffles and LDS, and its first lane then accepts the row -- the argmax
-// and the acceptance never leave the workgroup, so the step needs one launch and no device-wide
-// synchronisation.
+// Layout: the argmax takes one 256-thread workgroup per logit row (row_argmax_kernel): 128-bit loads of
+// the whole row issued together, max, sum and first index reduced through wave shuffles and LDS; then
+// accept_kernel accepts each slot with one thread.  Without an argmax output, or for vocabularies past
+// what 16 chunks per thread of 256 threads cover, one 1024-thread workgroup per slot reads the slot's T
+// rows in turn and its first lane accepts (greedy_accept_kernel): one launch, but the rows of a slot in
+// sequence, which costs more than the second launch.
 #include <limits.h>
 #include <math.h>
 
@@ -239,6 +240,86 @@ __global__ __launch_bounds__(kAcceptThreads) void greedy_accept_kernel(AcceptArg
   if (tid == 0) accept_row(a, b, [](int j) { return gsh[j]; });
 }
 
+// ---------------------------------------------------------------------------------------------- row argmax
+
+// The argmax alone, one 256-thread workgroup per logit row (rows x T workgroups instead of rows): the same rule
+// and arithmetic as greedy_accept_kernel, its result written to ``nxt_out``; accept_kernel then accepts.  Two
+// short launches instead of one long one: each row's read, three reductions and compare are a fraction of what
+// one workgroup per slot does for T rows in sequence.
+constexpr int kRowThreads = 256;
+constexpr int kRowWaves = kRowThreads / kWave;
+
+template <typename F, typename Op>
+__device__ __forceinline__ F row_reduce(F v, F* red, Op op) {
+  const int lane = lane_id(), wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, kWave));
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  F x = red[0];
+#pragma unroll
+  for (int w = 1; w < kRowWaves; ++w) x = op(x, red[w]);
+  __syncthreads();
+  return x;
+}
+
+template <typename L, int KPT, bool ALIGNED>
+__global__ __launch_bounds__(kRowThreads) void row_argmax_kernel(AcceptArgs a) {
+  using C = LogitChunk<L>;
+  constexpr int kE = C::kElems;
+  __shared__ float redf[kRowWaves];
+  __shared__ int redi[kRowWaves];
+  const int row = blockIdx.x;  // b * T + t
+  const int tid = threadIdx.x;
+  const int V = a.vocab;
+  const int nchunks = V / kE;
+  const L* rowp = reinterpret_cast<const L*>(a.logits) + (int64_t)row * a.logits_stride;
+  u32x4_t x[KPT];
+#pragma unroll
+  for (int k = 0; k < KPT; ++k) {
+    const int ci = tid + k * kRowThreads;
+    const bool ok = ci < nchunks;
+    if constexpr (ALIGNED)
+      x[k] = ok ? reinterpret_cast<const u32x4_t*>(rowp)[ci] : u32x4_t{0u, 0u, 0u, 0u};
+    else
+      x[k] = ok ? C::gather(rowp + (int64_t)ci * kE) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+  const int tail0 = nchunks * kE;
+  const bool has_tail = tid < V - tail0;
+  const float tail = has_tail ? C::scalar(rowp + tail0 + tid) : -INFINITY;
+  float m = tail;
+#pragma unroll
+  for (int k = 0; k < KPT; ++k)
+    if (tid + k * kRowThreads < nchunks) {
+#pragma unroll
+      for (int e = 0; e < kE; ++e) m = fmaxf(m, C::get(x[k], e));
+    }
+  m = row_reduce(m, redf, [](float p, float q) { return fmaxf(p, q); });
+  float sum = has_tail ? expf(tail - m) : 0.f;
+#pragma unroll
+  for (int k = 0; k < KPT; ++k)
+    if (tid + k * kRowThreads < nchunks) {
+#pragma unroll
+      for (int e = 0; e < kE; ++e) sum += expf(C::get(x[k], e) - m);
+    }
+  sum = row_reduce(sum, redf, [](float p, float q) { return p + q; });
+  const float lse = logf(sum);
+  const float top = C::round(0.f - lse);
+  int best = INT_MAX;
+#pragma unroll
+  for (int k = 0; k < KPT; ++k) {
+    const int ci = tid + k * kRowThreads;
+    if (ci < nchunks) {
+#pragma unroll
+      for (int e = kE - 1; e >= 0; --e)
+        if (C::round((C::get(x[k], e) - m) - lse) == top) best = min(best, ci * kE + e);
+    }
+  }
+  if (has_tail && C::round((tail - m) - lse) == top) best = min(best, tail0 + tid);
+  best = row_reduce(best, redi, [](int p, int q) { return min(p, q); });
+  if (tid == 0) a.nxt_out[row] = best == INT_MAX ? 0 : best;
+}
+
 }  // namespace omni
 
 using namespace omni;
@@ -327,6 +408,41 @@ extern "C" int omni_greedy_accept(const void* logits, int64_t logits_stride, int
   a.logits_stride = logits_stride;
   a.vocab = vocab;
   hipStream_t s = (hipStream_t)stream;
+  // Argmax by row, then the acceptance (when the argmaxes have somewhere to go and a row fits 16 chunks per
+  // thread of a 256-thread workgroup: vocabularies up to 32768 bf16 / 16384 fp32 entries).
+  const int64_t rkpt = (nchunks + kRowThreads - 1) / kRowThreads;
+  if (nxt && rkpt <= 16) {
+    const int rk = rkpt <= 1 ? 1 : rkpt <= 2 ? 2 : rkpt <= 4 ? 4 : rkpt <= 8 ? 8 : 16;
+    const int nrows = rows * tokens_per_row;
+#define OMNI_ROW_ARGMAX(L, K)                                                       \
+  do {                                                                              \
+    if (aligned) row_argmax_kernel<L, K, true><<<nrows, kRowThreads, 0, s>>>(a);    \
+    else row_argmax_kernel<L, K, false><<<nrows, kRowThreads, 0, s>>>(a);           \
+  } while (0)
+    if (logits_dtype == OMNI_BF16) {
+      switch (rk) {
+        case 1: OMNI_ROW_ARGMAX(uint16_t, 1); break;
+        case 2: OMNI_ROW_ARGMAX(uint16_t, 2); break;
+        case 4: OMNI_ROW_ARGMAX(uint16_t, 4); break;
+        case 8: OMNI_ROW_ARGMAX(uint16_t, 8); break;
+        default: OMNI_ROW_ARGMAX(uint16_t, 16); break;
+      }
+    } else {
+      switch (rk) {
+        case 1: OMNI_ROW_ARGMAX(float, 1); break;
+        case 2: OMNI_ROW_ARGMAX(float, 2); break;
+        case 4: OMNI_ROW_ARGMAX(float, 4); break;
+        case 8: OMNI_ROW_ARGMAX(float, 8); break;
+        default: OMNI_ROW_ARGMAX(float, 16); break;
+      }
+    }
+#undef OMNI_ROW_ARGMAX
+    st = omni_launch_status();
+    if (st != OMNI_OK) return st;
+    a.nxt_in = nxt;
+    accept_kernel<<<(rows + 63) / 64, 64, 0, s>>>(a, rows);
+    return omni_launch_status();
+  }
   const int k = kpt <= 1 ? 1 : kpt <= 2 ? 2 : kpt <= 4 ? 4 : kpt <= 8 ? 8 : 16;
   if (logits_dtype == OMNI_BF16) {
     switch (k) {

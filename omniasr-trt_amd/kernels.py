@@ -14,7 +14,7 @@ through its C ABI (``include/omniasr_mi355x.h``) on torch's current stream:
 
 Beyond the reference's functions, for the fused step: :func:`spec_prepare` (proposal plus the step's
 tokens / positions / cache rows / key counts in one launch) and :func:`greedy_accept` (the argmax of
-the verify logits and the acceptance in one launch).
+the verify logits and the acceptance).
 
 Nothing here synchronises or allocates beyond the outputs and the attention workspace (from torch's
 allocator, so from a graph's pool under capture), so every function can be captured in a HIP graph.
@@ -363,8 +363,8 @@ def greedy_accept(logits: torch.Tensor, tokens: torch.Tensor, out: torch.Tensor,
                   last: torch.Tensor, done: torch.Tensor, draft_next: torch.Tensor | None,
                   start: torch.Tensor | None, use_draft: torch.Tensor | None, limit: int, eos: int,
                   nxt: torch.Tensor | None = None) -> torch.Tensor:
-    """``F.log_softmax(logits, -1).argmax(-1)`` of the verify logits [B*T, V] followed by :func:`accept`, in one
-    launch (src/omniasr_trt/spec.py:106-108).  Returns the argmaxes [B, T] (written into ``nxt`` when given).
+    """``F.log_softmax(logits, -1).argmax(-1)`` of the verify logits [B*T, V] followed by :func:`accept`
+    (src/omniasr_trt/spec.py:106-108): an argmax workgroup per row, then the acceptance.  Returns the argmaxes [B, T] (written into ``nxt`` when given).
     ``draft_next`` / ``start`` / ``use_draft`` None: the one-token step's update (src/omniasr_trt/decode.py:218-224)."""
     lib = _lib.load()
     b, width = tokens.shape

@@ -301,13 +301,28 @@ def test_accept_golden_vectors(cuda):
             np.testing.assert_array_equal(d[name].cpu().numpy(), z[p + name + "_after"], err_msg=f"case {c} {name}")
 
 
-def test_greedy_accept_state_vs_oracle(cuda):
-    """Logits with planted argmaxes that confirm 0..k drafts, EOS and the limit: the state after the fused kernel
-    equals the oracle's acceptance of the oracle's argmaxes."""
+def _greedy_accept_no_nxt(x, tokens, out, tok, last, done, dn, start, use, limit, eos):
+    """``omni_greedy_accept`` with no argmax output (``nxt`` NULL): the one-launch kernel that argmaxes and accepts
+    each slot in one workgroup."""
+    b, t = tokens.shape
+    lib = kernels._lib.load()
+    st = lib.omni_greedy_accept(x.data_ptr(), x.stride(0), x.size(1), 1, tokens.data_ptr(), None,
+                                out.data_ptr(), out.stride(0), out.size(1), tok.data_ptr(), last.data_ptr(),
+                                done.data_ptr(), dn.data_ptr(), start.data_ptr(), use.data_ptr(), b, t, limit, eos,
+                                torch.cuda.current_stream().cuda_stream)
+    assert st == 0, st
+
+
+@pytest.mark.parametrize("path,v", [("rows", 10288), ("slot", 10288), ("slot", 40000)])
+def test_greedy_accept_state_vs_oracle(cuda, path, v):
+    """Logits with planted argmaxes that confirm 0..k drafts, EOS and the limit: the state after the kernel equals
+    the oracle's acceptance of the oracle's argmaxes.  ``rows``: the row-argmax launch then the acceptance (the
+    argmaxes are returned); ``slot``: one workgroup per slot (no argmax output at 10288, and the path a
+    vocabulary past 32768 bf16 entries takes)."""
     g = gen(10)
     rng = np.random.default_rng(10)
     for t in (1, 2, 5, 9):
-        b, v, cap = 8, 10288, 512
+        b, cap = 8, 512
         x = torch.randn(b * t, v, generator=g)
         tokens = torch.randint(3, v, (b, t), generator=g)
         for r in range(b):  # plant: the argmax after fed token j is fed token j+1 for the first `ok` positions
@@ -330,10 +345,13 @@ def test_greedy_accept_state_vs_oracle(cuda):
         nxt_o = ov.log_softmax_argmax(npf(x), "bf16").reshape(b, t)
         ov.accept(tokens.numpy(), nxt_o, o[0], o[1], o[2], o[3], o[4], start.numpy(), use.numpy(), 60, 2)
         d = [a.to(cuda) for a in (out, tok, last, done, dn)]
-        say(f"greedy_accept t={t}")
-        nxt = kernels.greedy_accept(x.to(cuda), tokens.to(cuda), d[0], d[1], d[2], d[3], d[4], start.to(cuda),
-                                    use.to(cuda), 60, 2)
-        np.testing.assert_array_equal(nxt.cpu().numpy(), nxt_o)
+        say(f"greedy_accept {path} v={v} t={t}")
+        if path == "slot" and v == 10288:
+            _greedy_accept_no_nxt(x.to(cuda), tokens.to(cuda), *d, start.to(cuda), use.to(cuda), 60, 2)
+        else:
+            nxt = kernels.greedy_accept(x.to(cuda), tokens.to(cuda), d[0], d[1], d[2], d[3], d[4], start.to(cuda),
+                                        use.to(cuda), 60, 2)
+            np.testing.assert_array_equal(nxt.cpu().numpy(), nxt_o)
         for got, want in zip(d, o):
             np.testing.assert_array_equal(got.cpu().numpy(), want)
 
