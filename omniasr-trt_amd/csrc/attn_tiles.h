@@ -36,17 +36,17 @@ struct KVTile {
 
 __device__ __forceinline__ u32x4_t ld16(const char* p) { return *reinterpret_cast<const u32x4_t*>(p); }
 
-// One 32-key tile of K and V into MFMA operand layout.  Key rows are contiguous (D elements apart), so each load is
-// the wave-uniform tile base plus a 32-bit lane offset.  K rows past ``kmax`` (the last cache position, relative to
+// One 32-key tile of K and V into MFMA operand layout.  Key rows are kRow bytes apart (contiguous rows of D elements
+// by default; a 128-dimension slice of a wider head otherwise), so each load is the wave-uniform tile base plus a
+// 32-bit lane offset.  K rows past ``kmax`` (the last cache position, relative to
 // the tile's first key; 31 inside the cache) are read at kmax; their scores are masked.  V rows at or past
 // ``vstop`` (the end of the keys in use, relative; 32 for a full tile, >= 1 for a tile that is attended) are read
 // at vstop - 1, a key in use: every query's probability of those keys is 0, and 0 times a finite value of a key in
 // use adds nothing (stale memory past the keys could hold NaN).  Only addresses are clamped, never loaded data, so
 // nothing waits for a tile's loads before its math.
-template <int D>
+template <int D, uint32_t kRow = D * 2>
 __device__ __forceinline__ void load_tile_clamped(KVTile<D>& t, const char* kt, const char* vt, int kmax, int vstop,
                                                   int c, int g) {
-  constexpr uint32_t kRow = D * 2;
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb) {
     int rk = 8 * (c >> 2) + 4 * mb + (c & 3);
@@ -130,13 +130,12 @@ struct SoftmaxState {
   float l_run;  // this lane's share of query c's probability sum (relative to m_ref)
 };
 
-// One tile: scores, the causal / end-of-row mask (key0 + j >= lim: query c does not see key j of this lane), the
-// lazy reference max, probabilities, O += P V.  The mask is a no-op on tiles every query sees whole.
+// A tile with its raw scores ``sv`` (lane (c, g): query c, keys key0 + j): the causal / end-of-row mask (key0 + j >=
+// lim: query c does not see key j of this lane), the lazy reference max, probabilities, O += P V.  The mask is a no-op
+// on tiles every query sees whole.
 template <int D>
-__device__ __forceinline__ void attend(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float c_scale,
-                                       SoftmaxState& st, f32x4_t (&o)[D / 16], int g, int key0, int lim) {
-  float sv[8];
-  tile_scores<D>(t, qop, sv);
+__device__ __forceinline__ void attend_scored(const KVTile<D>& t, float (&sv)[8], float c_scale, SoftmaxState& st,
+                                              f32x4_t (&o)[D / 16], int g, int key0, int lim) {
   bool over = false;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -162,6 +161,23 @@ __device__ __forceinline__ void attend(const KVTile<D>& t, const u32x4_t (&qop)[
     st.l_run += p[j];
   }
   tile_pv<D>(t, p, o);
+}
+
+// One tile: scores, then attend_scored.
+template <int D>
+__device__ __forceinline__ void attend(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float c_scale,
+                                       SoftmaxState& st, f32x4_t (&o)[D / 16], int g, int key0, int lim) {
+  float sv[8];
+  tile_scores<D>(t, qop, sv);
+  attend_scored<D>(t, sv, c_scale, st, o, g, key0, lim);
+}
+
+// A workgroup barrier ordering LDS accesses only: global loads in flight stay in flight across it (a full
+// __syncthreads waits for every outstanding memory access of the wave).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 }  // namespace omni

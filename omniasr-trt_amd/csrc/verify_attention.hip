@@ -16,8 +16,11 @@
 //    pipeline; a unit's two halves meet through partials written through to the coherence point and a ticket per
 //    unit, and the workgroup of the second half fetches the first while its waves finish.  One launch; results
 //    do not depend on timing.
-//  * Split-K (every other shape; verify_attn_mfma_kernel / verify_attn_valu_kernel): one wavefront per (key
-//    split, head, row), grid (splits, heads, rows).  A row's 32-key tiles are dealt round-robin over its splits.
+//  * Split-K (every other shape; verify_attn_mfma_kernel / verify_attn_slice_kernel / verify_attn_valu_kernel):
+//    one wavefront per (key split, head, row), grid (splits, heads, rows) -- for head dims 256 and 512 one
+//    workgroup of D/128 waves per split, a wave per 128-dimension slice, the partial scores added through LDS (the
+//    tile registers of the 128-dimension kernel, two tiles in flight, two waves per SIMD).  A row's 32-key tiles are
+//    dealt round-robin over its splits.
 //    Splits beyond a row's last key exit at once, so the grid depends on the key bucket only (graph capture)
 //    while ragged rows read just their own keys.  The splits' partials are merged by a second launch or by the
 //    last split to finish (ticket per (row, head)); a row with one split writes its output directly.
@@ -106,6 +109,12 @@ __device__ __forceinline__ void put_through2(float* p, float x, float y) {
   __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Four floats (16 bytes) written through to the coherence point as two 8-byte agent-scope stores.
+__device__ __forceinline__ void put_through4c(float* p, f32x4_t v) {
+  put_through2(p, v[0], v[1]);
+  put_through2(p + 2, v[2], v[3]);
+}
+
 // Partial slot of the q-th partial to merge: the row's key splits, then the generated-keys slot if any.
 __device__ __forceinline__ int merge_slot(const AttnArgs& a, int nact, int q) {
   return q < nact ? q : a.gen_split;
@@ -161,10 +170,12 @@ __device__ __forceinline__ f32x4_t get_through4(const float* p) {
 }
 
 template <typename OutT>
-__device__ void merge_splits_fast(const AttnArgs& a, int b, int h, int nact) {
+__device__ void merge_splits_fast(const AttnArgs& a, int b, int h, int nact, int d0 = 0, int dw = -1) {
   constexpr int kS = 8, kR = 3;
   const int lane = lane_id();
-  const int T = a.T, D = a.D, nf = T * D;
+  const int T = a.T, D = a.D;
+  if (dw < 0) dw = D;  // dimensions d0 .. d0 + dw - 1 of every query (dw a multiple of 4)
+  const int nf = T * dw;
   const int nq = nact + (a.gen_split >= 0 ? 1 : 0);
   const int64_t split0 = ((int64_t)b * a.H + h) * a.splits;
   OutT* out = reinterpret_cast<OutT*>(a.out);
@@ -189,13 +200,13 @@ __device__ void merge_splits_fast(const AttnArgs& a, int b, int h, int nact) {
           lv[sq][r] = 0.f;
           ov[sq][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
           if (q0 + sq < nq && f < nf) {
-            const int t = f / D;
+            const int t = f / dw;
             const int64_t slot = (split0 + merge_slot(a, nact, q0 + sq)) * T + t;
             const uint64_t ml = __hip_atomic_load(reinterpret_cast<uint64_t*>(a.part_ml + slot * 2), __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT);
             mv[sq][r] = __uint_as_float((uint32_t)ml);
             lv[sq][r] = __uint_as_float((uint32_t)(ml >> 32));
-            ov[sq][r] = get_through4(a.part_o + slot * D + (f - t * D));
+            ov[sq][r] = get_through4(a.part_o + slot * D + d0 + (f - t * dw));
           }
         }
       }
@@ -220,9 +231,9 @@ __device__ void merge_splits_fast(const AttnArgs& a, int b, int h, int nact) {
     for (int r = 0; r < kR; ++r) {
       const int f = f0 + r * 256 + 4 * lane;
       if (f >= nf) continue;
-      const int t = f / D;
+      const int t = f / dw;
       const float div = den[r] > 0.f ? den[r] : 1.f;
-      store4<OutT>(out + ((int64_t)(b * T + t) * a.H + h) * D + (f - t * D), acc[r] / div);
+      store4<OutT>(out + ((int64_t)(b * T + t) * a.H + h) * D + d0 + (f - t * dw), acc[r] / div);
     }
   }
 }
@@ -397,6 +408,150 @@ __global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(Attn
   finish_split<uint16_t>(a, b, h, r.nact);
 }
 
+// Split-K for head dims past 128 (256, 512): one workgroup of D/128 waves per (split, head, row), wave w holding
+// dimensions 128w .. 128w + 127 of q, K, V and O.  Each wave reads its slice of a tile (32 keys x 256 bytes of K
+// and of V; two tiles in flight, the register budget of the 128-dimension kernel), its partial scores go to LDS,
+// and after one barrier every wave adds the D/128 partials in slice order, so all waves hold the same scores and
+// the same softmax state; each then accumulates its own slice of P V.  Tiles are dealt to the splits as in
+// attend_split; the partials and the last split's merge are those of verify_attn_mfma_kernel.
+template <int D>
+__global__ __launch_bounds__(64 * (D / 128), 2) void verify_attn_slice_kernel(AttnArgs a) {
+  constexpr int NSL = D / 128;
+  __shared__ float sx[2][NSL][kWave * 8];  // partial scores of a tile by slice, double-buffered
+  __shared__ int s_ticket;
+  const int sp = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const SplitRange r = split_range(a, b, sp);
+  if (sp >= r.nact) return;  // uniform over the workgroup
+  const int lane = lane_id(), w = threadIdx.x / kWave, c = lane & 15, g = lane >> 4;
+  const int T = a.T;
+
+  u32x4_t qop[4];  // B operand of the slice's S^T = K Q^T: lane (c, g) holds q[c][128w + 32s + 8g .. + 7]
+  {
+    const uint16_t* qrow =
+        reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)(b * T + c) * a.H + h) * D + w * 128 + g * 8;
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2)
+      qop[s2] = c < T ? *reinterpret_cast<const u32x4_t*>(qrow + s2 * 32) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+  SoftmaxState st{-INFINITY, -INFINITY, 0.f};
+  f32x4_t o[8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t row_tiles = (r.total + 31) >> 5;
+  const int64_t first = sp;
+  const int64_t ntot = first < row_tiles ? (row_tiles - first + r.nact - 1) / r.nact : 0;
+  // The launcher sends only caches with contiguous key rows (s_pos == D) here.
+  const char* kt = reinterpret_cast<const char*>(a.k) + (b * a.s_row + h * a.s_head + first * 32 * D) * 2 + w * 256;
+  const char* vt = reinterpret_cast<const char*>(a.v) + (b * a.s_row + h * a.s_head + first * 32 * D) * 2 + w * 256;
+  const int64_t tile_bytes = (int64_t)r.nact * 32 * D * 2;
+  const int64_t last_key = a.cache_len - 1;
+  const int64_t own = r.n + (a.causal ? c : 0);
+  const int lim_c = (int)(own < r.total ? own : r.total);
+  auto load_k = [&](KVTile<128>& t, int64_t k) {
+    const int64_t kb = (first + k * r.nact) * 32;
+    const int64_t kmax = last_key - kb, vstop = r.total - kb;
+    load_tile_clamped<128, D * 2>(t, kt + k * tile_bytes, vt + k * tile_bytes, kmax < 31 ? (int)kmax : 31,
+                                  vstop < 32 ? (int)vstop : 32, c, g);
+  };
+  auto attend_k = [&](const KVTile<128>& t, int64_t k) {
+    float sv[8];
+    tile_scores<128>(t, qop, sv);
+    float* mine = &sx[k & 1][w][lane * 8];
+    *reinterpret_cast<f32x4_t*>(mine) = f32x4_t{sv[0], sv[1], sv[2], sv[3]};
+    *reinterpret_cast<f32x4_t*>(mine + 4) = f32x4_t{sv[4], sv[5], sv[6], sv[7]};
+    lds_barrier();
+    float tot[8];
+#pragma unroll
+    for (int ww = 0; ww < NSL; ++ww) {
+      const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(&sx[k & 1][ww][lane * 8]);
+      const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(&sx[k & 1][ww][lane * 8 + 4]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        tot[j] = ww == 0 ? lo[j] : tot[j] + lo[j];
+        tot[j + 4] = ww == 0 ? hi[j] : tot[j + 4] + hi[j];
+      }
+    }
+    attend_scored<128>(t, tot, a.scale_log2, st, o, g, (int)((first + k * r.nact) * 32) + 8 * g, lim_c);
+  };
+  // The buffer written for tile k was last read for tile k - 2, before every wave passed tile k - 1's barrier.
+  if (ntot > 0) {
+    KVTile<128> A, B;
+    load_k(A, 0);
+    int64_t k = 0;
+    for (; k + 2 < ntot; k += 2) {
+      load_k(B, k + 1);
+      attend_k(A, k);
+      load_k(A, k + 2);
+      attend_k(B, k + 1);
+    }
+    if (k + 1 < ntot) {
+      load_k(B, k + 1);
+      attend_k(A, k);
+      attend_k(B, k + 1);
+    } else {
+      attend_k(A, k);
+    }
+  }
+
+  // ---- finish: per-query sums (the same in every wave), then the output slice or this split's partial slice
+  float l_tot = st.l_run + __shfl_xor(st.l_run, 16, kWave);
+  l_tot += __shfl_xor(l_tot, 32, kWave);
+  float li[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) li[i] = __shfl(l_tot, 4 * g + i, kWave);
+  if (r.nact == 1 && a.gen_split < 0) {
+    uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 4 * g + i;
+      if (t >= T) continue;
+      const float div = li[i] > 0.f ? li[i] : 1.f;
+      u32x4_t wv;
+#pragma unroll
+      for (int q2 = 0; q2 < 4; ++q2) wv[q2] = pack_bf16x2(o[2 * q2][i] / div, o[2 * q2 + 1][i] / div);
+      *reinterpret_cast<u32x4_t*>(out + ((int64_t)(b * T + t) * a.H + h) * D + w * 128 + c * 8) = wv;
+    }
+    return;
+  }
+  const int64_t base = (((int64_t)b * a.H + h) * a.splits + sp) * T;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = 4 * g + i;
+    if (t >= T) continue;
+    float* po = a.part_o + (base + t) * D + w * 128 + c * 8;
+    const f32x4_t x0 = f32x4_t{o[0][i], o[1][i], o[2][i], o[3][i]};
+    const f32x4_t x1 = f32x4_t{o[4][i], o[5][i], o[6][i], o[7][i]};
+    if (a.separate) {
+      reinterpret_cast<f32x4_t*>(po)[0] = x0;
+      reinterpret_cast<f32x4_t*>(po)[1] = x1;
+    } else {
+      put_through4c(po, x0);
+      put_through4c(po + 4, x1);
+    }
+  }
+  if (w == 0 && g == 0 && c < T) {
+    if (a.separate) {
+      a.part_ml[(base + c) * 2] = st.m_ref;
+      a.part_ml[(base + c) * 2 + 1] = l_tot;
+    } else {
+      put_through2(a.part_ml + (base + c) * 2, st.m_ref, l_tot);
+    }
+  }
+  if (a.separate) return;
+  // Every wave's partial stores have reached the coherence point before the split's ticket is taken.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  int* counter = &a.counters[b * a.H + h];
+  if (threadIdx.x == 0) s_ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (s_ticket != r.nact - 1) return;
+  merge_splits_fast<uint16_t>(a, b, h, r.nact, w * 128, 128);  // each wave its slice
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------------------------------------- workgroup per row
 
 constexpr int kWgWaves = 8;
@@ -410,13 +565,6 @@ constexpr int64_t kPairMaxQueryRows = int64_t{1} << 30;  // query rows x heads: 
 __device__ __forceinline__ int row_tile_count(const AttnArgs& a, int b) {
   const SplitRange r = split_range(a, b, 0);
   return (int)((r.total + 31) >> 5);
-}
-
-// Two floats x 2 (16 bytes) written through to the coherence point as two 8-byte agent-scope stores.  Unlike
-// put_through4 these are stores the compiler counts, so a later wait for older loads does not wait for them.
-__device__ __forceinline__ void put_through4c(float* p, f32x4_t v) {
-  put_through2(p, v[0], v[1]);
-  put_through2(p + 2, v[2], v[3]);
 }
 
 // One partial (m, l, O[t][d .. d + 3]) read at the coherence point.
@@ -982,8 +1130,8 @@ extern "C" int32_t omni_verify_attention_chunk(int32_t rows, int32_t tokens, int
   // About 2048 waves (8 per CU) when the rows are full, at most 8 tiles (256 keys) per split: measured on
   // config 3 (8 rows x 32 heads, 750-2400 keys), 224-256 keys per split are among the fastest and longer
   // splits leave too few waves in flight; at least 64 keys so that a split's fixed cost stays small.  Head dims
-  // of 256 and more run one wave per SIMD with a whole tile in registers: 256 keys per split (measured at the real
-  // checkpoint's 8 slots x 8 heads x 512: 47.7 us against 63.6 us for 96-key splits).
+  // of 256 and more: 256 keys per split (measured at the real checkpoint's 8 slots x 8 heads x 512, T = 5, with the
+  // merge launch: 45.6 us against 49.0 us for 128-key splits).
   const int64_t items = (int64_t)rows * heads;
   int64_t chunk = ((int64_t)keys * items + 2047) / 2048;
   chunk = (chunk + 31) / 32 * 32;
@@ -995,10 +1143,10 @@ extern "C" int32_t omni_verify_attention_chunk(int32_t rows, int32_t tokens, int
 
 static size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
-// Partial slots per unit in the workspace: split-K at this chunk, or stream-K.
+// Partial slots per unit in the workspace: split-K at this chunk, or a unit's two halves.
 static size_t attn_slots(int keys, int chunk) {
   const int splits = attn_splits(keys, chunk);
-  return (size_t)(splits > 2 ? splits : 2);  // split-K's splits, or a unit's two halves
+  return (size_t)(splits > 2 ? splits : 2);
 }
 
 extern "C" size_t omni_verify_attention_workspace(int32_t rows, int32_t tokens, int32_t heads,
@@ -1016,8 +1164,8 @@ static int launch_attention(const AttnArgs& a, int rows, int dtype, hipStream_t 
   if (mfma) {
     switch (a.D) {
       case 128: verify_attn_mfma_kernel<128, true><<<grid, 64, 0, s>>>(a); break;
-      case 256: verify_attn_mfma_kernel<256, false><<<grid, 64, 0, s>>>(a); break;
-      case 512: verify_attn_mfma_kernel<512, false><<<grid, 64, 0, s>>>(a); break;
+      case 256: verify_attn_slice_kernel<256><<<grid, 128, 0, s>>>(a); break;
+      case 512: verify_attn_slice_kernel<512><<<grid, 256, 0, s>>>(a); break;
       default: verify_attn_valu_kernel<uint16_t><<<grid, 64, 0, s>>>(a); break;
     }
   } else if (dtype == OMNI_BF16) {
