@@ -229,14 +229,27 @@ def time_small_kernels(pkg, torch, dec, reps: int = 200) -> dict:
     vc = torch.zeros_like(kc)
 
     def timed(fn, n):
+        """Device time per call: ``n`` calls captured in one graph, replayed between HIP events on the capture stream
+        (eager calls would time the host's launch rate for kernels this short)."""
         fn()
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(n):
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
             fn()
-        e1.record()
-        torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            graph.capture_begin()
+            for _ in range(n):
+                fn()
+            graph.capture_end()
+            graph.replay()
+            stream.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            graph.replay()
+            e1.record(stream)
+            stream.synchronize()
+        torch.cuda.current_stream().wait_stream(stream)
         return e0.elapsed_time(e1) * 1000.0 / n
 
     for name, tokens_per_slot in (("rope_kv_config2", 5), ("rope_kv_prefill_8x2048", 2048)):
