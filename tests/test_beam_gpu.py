@@ -55,7 +55,7 @@ def _beam_case(cuda, dtype, groups, beams, h, d, cap, gcap, ctx_len, gen_len, ct
 
 
 @pytest.mark.parametrize("beams", [1, 3, 5])
-@pytest.mark.parametrize("d", [128, 64, 512])
+@pytest.mark.parametrize("d", [128, 64, 256, 512])
 def test_beam_attention_bf16(cuda, beams, d):
     """The reference's case (tests/test_kernels.py:98-126): a finished input reads nothing, ragged generated
     lengths, pointers anywhere in the generated rows."""

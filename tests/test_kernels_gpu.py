@@ -115,6 +115,7 @@ def test_verify_attention_bf16(cuda, t):
     lengths = torch.tensor([600, 257, 1, 0])  # 0: a finished row (query i then sees keys [0, i))
     _attn_case(cuda, torch.bfloat16, 4, 8, 128, t, 700, lengths, 640, 2, BF16_TOL)
     _attn_case(cuda, torch.bfloat16, 4, 8, 512, t, 700, lengths, 640, 3, BF16_TOL)
+    _attn_case(cuda, torch.bfloat16, 4, 4, 256, t, 700, lengths, 640, 5, BF16_TOL)  # two 128-dimension slices
 
 
 @pytest.mark.parametrize("width", [1, 15, 64, 97, 300])
@@ -177,7 +178,8 @@ def test_verify_attention_workgroup_and_split_k(cuda, t):
 def test_verify_attention_split_choices_agree(cuda):
     """Every split size and both merge modes give the oracle's result, and the two merge modes agree."""
     lengths = torch.tensor([1500, 3, 700, 64, 0, 1023])
-    for dtype, d, tol in ((torch.bfloat16, 128, BF16_TOL), (torch.float32, 16, F32_TOL), (torch.bfloat16, 512, BF16_TOL)):
+    for dtype, d, tol in ((torch.bfloat16, 128, BF16_TOL), (torch.float32, 16, F32_TOL), (torch.bfloat16, 512, BF16_TOL),
+                          (torch.bfloat16, 256, BF16_TOL)):
         for chunk in (64, 128, 320, 1536):
             a = _attn_case(cuda, dtype, 6, 4, d, 5, 1536, lengths, 1536, 7, tol, chunk=chunk, separate=False)
             b = _attn_case(cuda, dtype, 6, 4, d, 5, 1536, lengths, 1536, 7, tol, chunk=chunk, separate=True)
@@ -190,6 +192,10 @@ def test_verify_attention_tickets_left_zero(cuda):
     kc = torch.randn(2, 8, 1024, 128, device=cuda, dtype=torch.bfloat16)
     for _ in range(3):
         kernels.draft_attention(q, kc, kc, lengths, 5, 1024, 0.1, chunk=64)
+    q4 = torch.randn(10, 2, 512, device=cuda, dtype=torch.bfloat16)  # the wide-head kernel's in-kernel merge
+    kc4 = torch.randn(2, 2, 1024, 512, device=cuda, dtype=torch.bfloat16)
+    for _ in range(3):
+        kernels.draft_attention(q4, kc4, kc4, lengths, 5, 1024, 0.1, chunk=64, separate=False)
     torch.cuda.synchronize()
     assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
 
