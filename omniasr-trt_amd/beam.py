@@ -136,9 +136,9 @@ class BeamDecoder(GreedyDecoder):
             q = kernels.rope_kv(qkv, m.rope, pos, self.kg[i], self.vg[i], self.heads, None, j)
             o = kernels.beam_attention(q, self.kc[i], self.vc[i], ctx_len, self.kg[i], self.vg[i], ptr, gen_len, n,
                                        ckeys, scale).reshape(r, -1)
-            h = torch.addmm(h, o, out_w.t())
+            h.addmm_(o, out_w.t())  # in place: the GEMM adds into the residual, no copy of it
             gate, inner = (layer.ffn_layer_norm(h) @ gi_w.t()).chunk(2, -1)
-            h = torch.addmm(h, inner * F.silu(gate), ffo_w.t())
+            h.addmm_(inner * F.silu(gate), ffo_w.t())
         logp = F.log_softmax(m.final_proj(m.llama_decoder.layer_norm(h)), dim=-1)  # [R, V], model dtype
         vocab = logp.size(-1)
         if self.length_norm:

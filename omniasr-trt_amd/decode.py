@@ -168,9 +168,9 @@ class GreedyDecoder:
                 v = v_cache[i, :b, :, :width] if rows is None else v_cache[i, rows, :, :width]
                 o = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True).to(self.dtype)
                 o = o.transpose(1, 2).reshape(b * width, -1)
-            h = torch.addmm(h, o, out_w.t())
+            h.addmm_(o, out_w.t())  # in place: the GEMM adds into the residual, no copy of it
             gate, inner = (layer.ffn_layer_norm(h) @ gi_w.t()).chunk(2, -1)
-            h = torch.addmm(h, inner * F.silu(gate), ffo_w.t())
+            h.addmm_(inner * F.silu(gate), ffo_w.t())
         h = h.view(b, width, -1)
         last = h[torch.arange(b, device=self.device), torch.tensor(lens, device=self.device) - 1]
         logits = m.final_proj(m.llama_decoder.layer_norm(last))
@@ -190,9 +190,9 @@ class GreedyDecoder:
             qkv = layer.self_attn_layer_norm(h) @ qkv_w.t()
             q = kernels.rope_kv(qkv, m.rope, pos, self.k[i], self.v[i], self.heads, slots)
             o = kernels.draft_attention(q, self.k[i], self.v[i], lengths, tokens, keys, scale).reshape(rows, -1)
-            h = torch.addmm(h, o, out_w.t())
+            h.addmm_(o, out_w.t())  # in place: the GEMM adds into the residual, no copy of it
             gate, inner = (layer.ffn_layer_norm(h) @ gi_w.t()).chunk(2, -1)
-            h = torch.addmm(h, inner * F.silu(gate), ffo_w.t())
+            h.addmm_(inner * F.silu(gate), ffo_w.t())
         return m.final_proj(m.llama_decoder.layer_norm(h))
 
     def step(self, b: int, keys: int) -> None:
