@@ -370,6 +370,53 @@ def beam_leg(pkg, torch, w: Workload, steps: int, warmup: int, reps: int) -> dic
     return res
 
 
+def time_beam_attention(pkg, torch, reps: int, layers: int = 12, seed: int = 1006) -> dict:
+    """Config 5b's beam attention without the decoder: 8 inputs x 5 beams, contexts U[750, 2400] and 64 generated
+    keys per row (pointers to random rows), 32 heads x 128, bf16; 12 disjoint cache sets cycled (2.6 GB) so the
+    Infinity Cache cannot serve them; HIP events around graph replays of 24 launches."""
+    kernels = pkg.kernels
+    groups, heads, dim, gen, cap, gcap = SLOTS, 32, 128, 64, 2560, 128
+    rows = groups * BEAMS
+    rng = np.random.default_rng(seed)
+    lengths = rng.integers(750, 2401, groups)
+    ckeys = -(-int(lengths.max()) // 256) * 256
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    mk = lambda *shape: torch.randn(*shape, device="cuda", generator=g).to(torch.bfloat16)
+    sets = [(mk(groups, heads, cap, dim), mk(groups, heads, cap, dim), mk(rows, heads, gcap, dim),
+             mk(rows, heads, gcap, dim)) for _ in range(layers)]
+    q = mk(rows, heads, dim)
+    ctx_len = torch.tensor(lengths, device="cuda")
+    gen_len = torch.full((rows,), gen, device="cuda", dtype=torch.long)
+    ptr = torch.randint(0, rows, (rows, gcap), device="cuda", generator=g, dtype=torch.int32)
+    scale = dim ** -0.5
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        call = lambda i: kernels.beam_attention(q, *sets[i][:2], ctx_len, *sets[i][2:], ptr, gen_len, BEAMS, ckeys,
+                                                scale)
+        for i in range(layers):
+            call(i)
+        graph = torch.cuda.CUDAGraph()
+        graph.capture_begin()
+        for j in range(2 * layers):
+            call(j % layers)
+        graph.capture_end()
+        graph.replay()
+        stream.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+        stream.synchronize()
+    torch.cuda.current_stream().wait_stream(stream)
+    us = e0.elapsed_time(e1) * 1000.0 / (reps * 2 * layers)
+    nbytes = beam_attention_bytes(lengths, gen, rows, heads, dim)
+    return {"workload": "config 5b beam attention: 8 inputs x 5 beams, contexts U[750, 2400], 64 generated keys",
+            "us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1),
+            "frac_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "ctx_keys": ckeys, "launches": reps * 2 * layers}
+
+
 class AttentionCaches:
     """Config 3 without the decoder: 12 disjoint bf16 K/V sets [8, 32, 2560, 128] (2.5 GB touched per cycle: the
     256 MB Infinity Cache cannot serve them) standing in for the 12 layers' caches; ``heads`` / ``dim`` 8 / 512 give
@@ -474,6 +521,11 @@ def main() -> int:
     p.add_argument("--no-extra", action="store_true", help="skip the per-kernel figures")
     p.add_argument("--attention-only", action="store_true",
                    help="only the verify attention on config 3 (synthetic caches, no decoder) and a reference copy")
+    p.add_argument("--heads", type=int, default=32, help="--attention-only: heads (8 with --head-dim 512: the real "
+                   "checkpoint's shape)")
+    p.add_argument("--head-dim", type=int, default=128, help="--attention-only: head dim")
+    p.add_argument("--beam", action="store_true", help="--attention-only: the beam attention of config 5b instead "
+                   "(synthetic caches)")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box has one MI355X and the step shards by slot with no exchange "
@@ -485,9 +537,16 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X", file=sys.stderr)
         return 2
+    if args.attention_only and args.beam:
+        with torch.inference_mode():
+            ref = copy_reference(torch)
+            beam = time_beam_attention(pkg, torch, args.attn_reps)
+        print(json.dumps({"metric": "beam-attn HBM GB/s (% peak)", "value": beam["GBps"], "unit": "GB/s", "n_gpus": 1,
+                          "frac_peak": beam["frac_peak"], "beam_attention": beam, "copy_reference": ref}), flush=True)
+        return 0
     if args.attention_only:
         with torch.inference_mode():
-            caches = AttentionCaches(torch)
+            caches = AttentionCaches(torch, heads=args.heads, dim=args.head_dim)
             ref = copy_reference(torch)
             attn = time_attention(pkg, torch, caches, DRAFT + 1, args.attn_reps)
             sweep = [] if args.no_extra else [time_attention(pkg, torch, caches, t, args.attn_reps) for t in (1, 3, 9)]
