@@ -16,9 +16,13 @@ namespace omni {
 // builds the V operands once, then runs S^T = K Q^T, the lazy softmax (causal limit as the key limit) and
 // O += P V for every group that sees the tile.
 constexpr int kPfWaves = 4;
-constexpr int kPfSub = 2;  // 16-query groups per wave
+constexpr int kPfSub = 3;  // 16-query groups per wave (3: 255 VGPRs, two waves per SIMD; measured fastest of 1-4)
 constexpr int kPfQueries = 16 * kPfSub * kPfWaves;
 constexpr int kPfRow = 128 * 2 + 16;  // LDS bytes per key row: 256 B of data, padded against bank conflicts
+constexpr int kPfStage = 32;          // keys per LDS stage (one barrier each), a multiple of the 32-key MFMA tile
+constexpr int kPfThreads = 64 * kPfWaves;
+constexpr int kPfChunks = kPfStage * 16 / kPfThreads;  // 16-byte chunks of K (and of V) per thread per stage
+static_assert(kPfChunks * kPfThreads == kPfStage * 16, "a stage is whole chunks per thread");
 
 struct PrefillArgs {
   const uint16_t* q;    // [B * width, H, 128] bf16
@@ -70,7 +74,7 @@ __device__ __forceinline__ u32x4_t softmax_tile(float (&sv)[8], float c_scale, S
 __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attn_kernel(
     PrefillArgs a) {
   constexpr int D = 128, KS = D / 32;
-  __shared__ __attribute__((aligned(16))) char lds[2][2][32 * kPfRow];  // [buffer][K, V][key rows]
+  __shared__ __attribute__((aligned(16))) char lds[2][2][kPfStage * kPfRow];  // [buffer][K, V][key rows]
   const int nqb = (a.width + kPfQueries - 1) / kPfQueries;
   const int qb = (nqb - 1 - (int)blockIdx.x) * kPfQueries;  // the longest blocks first
   const int h = blockIdx.y, b = blockIdx.z;
@@ -80,26 +84,26 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
   const uint16_t* kbase = a.k + slot * a.s_row + h * a.s_head;
   const uint16_t* vbase = a.v + slot * a.s_row + h * a.s_head;
   const int kend = min(qb + kPfQueries, a.width);  // keys the block's last query sees
-  const int nt = (kend + 31) >> 5;
+  const int nt = (kend + kPfStage - 1) / kPfStage;
 
-  // Global -> LDS: thread tid moves 16-byte chunks tid and tid + 256 of the tile's K and of its V (32 rows x 256 B
-  // each).  Rows past the context read its last key (finite: masked by the causal limit, never NaN).
-  u32x4_t stage[4];
+  // Global -> LDS: thread tid moves 16-byte chunks tid, tid + kPfThreads, ... of the stage's K and of its V (kPfStage rows x
+  // 256 B each).  Rows past the context read its last key (finite: masked by the causal limit, never NaN).
+  u32x4_t stage[2 * kPfChunks];
   auto fetch = [&](int t) {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int ci = tid + e * 256, r = ci >> 4, col = ci & 15;
-      const int key = min(t * 32 + r, a.width - 1);
+    for (int e = 0; e < kPfChunks; ++e) {
+      const int ci = tid + e * kPfThreads, r = ci >> 4, col = ci & 15;
+      const int key = min(t * kPfStage + r, a.width - 1);
       stage[e] = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)key * D + col * 8);
-      stage[2 + e] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)key * D + col * 8);
+      stage[kPfChunks + e] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)key * D + col * 8);
     }
   };
   auto put = [&](int buf) {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int ci = tid + e * 256, r = ci >> 4, col = ci & 15;
+    for (int e = 0; e < kPfChunks; ++e) {
+      const int ci = tid + e * kPfThreads, r = ci >> 4, col = ci & 15;
       *reinterpret_cast<u32x4_t*>(&lds[buf][0][r * kPfRow + col * 16]) = stage[e];
-      *reinterpret_cast<u32x4_t*>(&lds[buf][1][r * kPfRow + col * 16]) = stage[2 + e];
+      *reinterpret_cast<u32x4_t*>(&lds[buf][1][r * kPfRow + col * 16]) = stage[kPfChunks + e];
     }
   };
 
@@ -126,17 +130,21 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
   __syncthreads();
   for (int t = 0; t < nt; ++t) {
     fetch(t + 1 < nt ? t + 1 : t);  // unconditional: the last iteration re-reads its own tile (cache hit)
+    // The stage's 32-key MFMA tiles in turn.
+#pragma unroll
+    for (int sub = 0; sub < kPfStage / 32; ++sub) {
+    const int key0 = t * kPfStage + sub * 32;
     // Groups that see the tile (wave-uniform): a live group whose last query reaches the tile's first key.
     bool act[kPfSub];
     bool any = false;
 #pragma unroll
     for (int u = 0; u < kPfSub; ++u) {
-      act[u] = q0[u] < a.width && t * 32 <= q0[u] + 15;
+      act[u] = q0[u] < a.width && key0 <= q0[u] + 15;
       any |= act[u];
     }
     if (any) {
-      const char* kl = lds[t & 1][0];
-      const char* vl = lds[t & 1][1];
+      const char* kl = lds[t & 1][0] + sub * 32 * kPfRow;
+      const char* vl = lds[t & 1][1] + sub * 32 * kPfRow;
       u32x4_t pop[kPfSub];
       {
         u32x4_t kf[2][KS];
@@ -162,7 +170,7 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
           float sv[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) sv[j] = sacc[j >> 2][j & 3];
-          pop[u] = softmax_tile<D / 16>(sv, a.scale_log2, st[u], o[u], g, t * 32 + 8 * g, q0[u] + c + 1);
+          pop[u] = softmax_tile<D / 16>(sv, a.scale_log2, st[u], o[u], g, key0 + 8 * g, q0[u] + c + 1);
         }
       }
       u32x4_t vf[8];
@@ -181,6 +189,7 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
                                                             __builtin_bit_cast(bf16x8_t, bop), o[u][e], 0, 0, 0);
         }
       }
+    }
     }
     put((t + 1) & 1);
     __syncthreads();

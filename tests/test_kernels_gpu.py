@@ -122,7 +122,7 @@ def test_verify_attention_bf16(cuda, t):
 def test_prefill_attention(cuda, width):
     """Causal attention over whole contexts (src/omniasr_trt/decode.py:163-164) against the oracle's verify attention
     with query p of a context over keys [0, p]: cache rows addressed through slots, widths that are not multiples
-    of the 64-query block or the 32-key tile."""
+    of the 192-query block or the 32-key tile."""
     g = gen(60 + width)
     b, h, d, rows, cap = 3, 4, 128, 5, 320
     kc = torch.randn(rows, h, cap, d, generator=g).to(torch.bfloat16)
