@@ -39,13 +39,14 @@ struct PrefillArgs {
 // 8 probabilities packed as the P operand.  (The same arithmetic as attend().)
 template <int NB>
 __device__ __forceinline__ u32x4_t softmax_tile(float (&sv)[8], float c_scale, SoftmaxState& st, f32x4_t (&o)[NB],
-                                                int g, int key0, int lim) {
+                                                int g, int key0, int lim, bool whole) {
   bool over = false;
+  if (!whole) {  // whole (wave-uniform): every query of the group sees every key of the tile
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    sv[j] = key0 + j < lim ? sv[j] : -INFINITY;
-    over |= sv[j] > st.thr;
+    for (int j = 0; j < 8; ++j) sv[j] = key0 + j < lim ? sv[j] : -INFINITY;
   }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) over |= sv[j] > st.thr;
   if (__any(over)) {
     float mx = sv[0];
 #pragma unroll
@@ -170,7 +171,8 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
           float sv[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) sv[j] = sacc[j >> 2][j & 3];
-          pop[u] = softmax_tile<D / 16>(sv, a.scale_log2, st[u], o[u], g, key0 + 8 * g, q0[u] + c + 1);
+          pop[u] = softmax_tile<D / 16>(sv, a.scale_log2, st[u], o[u], g, key0 + 8 * g, q0[u] + c + 1,
+                                        key0 + 31 <= q0[u]);
         }
       }
       u32x4_t vf[8];
