@@ -12,15 +12,18 @@ namespace omni {
 // Causal attention over whole contexts (the prefill): query p of context b attends to keys [0, p] of its cache row.
 // One workgroup of kPfWaves waves per (query block, head, context), the longest blocks first.  The block's 32-key
 // tiles go through LDS once for all of its waves (double-buffered: tile t + 1's global loads are in flight during
-// tile t's math).  Each wave holds kPfSub groups of 16 queries: per tile it reads the K / V fragments from LDS and
-// builds the V operands once, then runs S^T = K Q^T, the lazy softmax (causal limit as the key limit) and
-// O += P V for every group that sees the tile.
+// tile t's math).  Each wave holds kPfSub groups of 16 queries: per tile it reads the K fragments and, by LDS
+// transpose reads, the V operands once, then runs S^T = K Q^T, the lazy softmax (causal limit as the key limit,
+// skipped on tiles the whole group sees) and O += P V for every group that sees the tile.
 constexpr int kPfWaves = 4;
 constexpr int kPfSub = 3;  // 16-query groups per wave (3: 255 VGPRs, two waves per SIMD; measured fastest of 1-4)
 constexpr int kPfQueries = 16 * kPfSub * kPfWaves;
 constexpr int kPfRow = 128 * 2 + 16;  // LDS bytes per key row: 256 B of data, padded against bank conflicts
 constexpr int kPfStage = 32;          // keys per LDS stage (one barrier each), a multiple of the 32-key MFMA tile
 constexpr int kPfThreads = 64 * kPfWaves;
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16;
+typedef __attribute__((address_space(3))) const char lds_char;
 constexpr int kPfChunks = kPfStage * 16 / kPfThreads;  // 16-byte chunks of K (and of V) per thread per stage
 static_assert(kPfChunks * kPfThreads == kPfStage * 16, "a stage is whole chunks per thread");
 
@@ -175,20 +178,28 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
                                         key0 + 31 <= q0[u]);
         }
       }
-      u32x4_t vf[8];
+      {
+        // V operands by transpose reads: in lane group g (keys 8g .. 8g + 7) lane 4r + q points at key
+        // 8g + 4h + r, dimensions 16e + 4q .. 16e + 4q + 3 (h = 0, 1), and ds_read_b64_tr_b16 hands lane c the
+        // four keys' dimension 16e + c: block e's B operand, output column c = dimension 16e + c.
+        const int rr = c >> 2, q4 = c & 3;
+        const lds_char* vls = (const lds_char*)vl;  // vl points into LDS
 #pragma unroll
-      for (int j = 0; j < 8; ++j) vf[j] = *reinterpret_cast<const u32x4_t*>(vl + (8 * g + j) * kPfRow + c * 16);
+        for (int e = 0; e < 8; ++e) {
+          const int off = (8 * g + rr) * kPfRow + (16 * e + 4 * q4) * 2;
+          const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vls + off));
+          const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vls + off + 4 * kPfRow));
+          u32x4_t bop;
+          bop[0] = (uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
+          bop[1] = (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
+          bop[2] = (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
+          bop[3] = (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        u32x4_t bop;
-#pragma unroll
-        for (int w2 = 0; w2 < 4; ++w2)
-          bop[w2] = __builtin_amdgcn_perm(vf[2 * w2 + 1][e >> 1], vf[2 * w2][e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
-#pragma unroll
-        for (int u = 0; u < kPfSub; ++u) {
-          if (!act[u]) continue;
-          o[u][e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pop[u]),
-                                                            __builtin_bit_cast(bf16x8_t, bop), o[u][e], 0, 0, 0);
+          for (int u = 0; u < kPfSub; ++u) {
+            if (!act[u]) continue;
+            o[u][e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pop[u]),
+                                                              __builtin_bit_cast(bf16x8_t, bop), o[u][e], 0, 0, 0);
+          }
         }
       }
     }
@@ -208,10 +219,9 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
       const int qq = q0[u] + 4 * g + i;
       if (qq >= a.width) continue;
       const float div = li > 0.f ? li : 1.f;
-      u32x4_t wv;
+      uint16_t* orow = a.out + ((int64_t)(b * a.width + qq) * a.H + h) * D;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) wv[e] = pack_bf16x2(o[u][2 * e][i] / div, o[u][2 * e + 1][i] / div);
-      *reinterpret_cast<u32x4_t*>(a.out + ((int64_t)(b * a.width + qq) * a.H + h) * D + c * 8) = wv;
+      for (int e = 0; e < 8; ++e) orow[16 * e + c] = (uint16_t)pack_bf16x2(o[u][e][i] / div, 0.f);  // dim 16e + c
     }
   }
 }
