@@ -1057,7 +1057,6 @@ __global__ __launch_bounds__(64) void verify_attn_valu_kernel(AttnArgs a) {
 
 // Second launch of the split merge: one wave per (query row t, head, row b), every load issued at once (one
 // memory round trip).  Lane s holds split s's (m, l); each lane keeps D/64 output dimensions of every split.
-constexpr int kCombineMaxSplits = 32;
 
 template <typename OutT, int DPL>
 __global__ __launch_bounds__(64) void verify_attn_combine_kernel(AttnArgs a) {
@@ -1070,21 +1069,36 @@ __global__ __launch_bounds__(64) void verify_attn_combine_kernel(AttnArgs a) {
   const int T = a.T, D = a.D;
   const int64_t split0 = ((int64_t)b * a.H + h) * a.splits;
   OutT* orow = reinterpret_cast<OutT*>(a.out) + ((int64_t)(b * T + t) * a.H + h) * D;
-  if (nq > kCombineMaxSplits) {  // beyond the unrolled case: the generic merge
+  if (nq > kWave) {  // more partials than lanes to hold their (m, l): the generic merge
     if (t == 0) merge_splits<OutT>(a, b, h, nact);
     return;
   }
-  const int d0 = lane * DPL;
-  const bool has_d = d0 < D;
-  float po[kCombineMaxSplits][DPL];
+  const bool has_d = lane * DPL < D;
+  const int d0 = has_d ? lane * DPL : 0;  // lanes past the head's dimensions read dimension 0 and store nothing
+  // The splits' rows in batches of kB, every load of a batch in flight at once (addresses clamped to the last
+  // split; the clamped repeats are not added), added in split order.  The first batch is issued before the
+  // splits' (m, l), which the weights need, so a merge of up to kB splits is one memory round trip.
+  constexpr int kB = 16;  // one batch for up to 16 splits (the default chunk gives at most 10 at 2560 keys)
+  float po[kB][DPL];
+  auto load_batch = [&](int s0) {
 #pragma unroll
-  for (int s = 0; s < kCombineMaxSplits; ++s) {
-    if (s < nq && has_d) {
-      const float* src = a.part_o + ((split0 + merge_slot(a, nact, s)) * T + t) * D + d0;
+    for (int j = 0; j < kB; ++j) {
+      const int sj = s0 + j < nq ? s0 + j : nq - 1;
+      const float* src = a.part_o + ((split0 + merge_slot(a, nact, sj)) * T + t) * D + d0;
+      if constexpr (DPL % 4 == 0) {
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) po[s][e] = src[e];
+        for (int e4 = 0; e4 < DPL; e4 += 4) {
+          const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(src + e4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) po[j][e4 + e] = v4[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) po[j][e] = src[e];
+      }
     }
-  }
+  };
+  load_batch(0);
   float m = -INFINITY, l = 0.f;
   if (lane < nq) {
     const int64_t ml = ((split0 + merge_slot(a, nact, lane)) * T + t) * 2;
@@ -1098,13 +1112,17 @@ __global__ __launch_bounds__(64) void verify_attn_combine_kernel(AttnArgs a) {
   float acc[DPL];
 #pragma unroll
   for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+  for (int s0 = 0;; s0 += kB) {
 #pragma unroll
-  for (int s = 0; s < kCombineMaxSplits; ++s) {
-    if (s < nq) {
-      const float ws = __shfl(w, s, kWave);
+    for (int j = 0; j < kB; ++j) {
+      if (s0 + j < nq) {
+        const float ws = __shfl(w, s0 + j, kWave);
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) acc[e] += ws * po[s][e];
+        for (int e = 0; e < DPL; ++e) acc[e] += ws * po[j][e];
+      }
     }
+    if (s0 + kB >= nq) break;
+    load_batch(s0 + kB);
   }
   if (!has_d) return;
 #pragma unroll
