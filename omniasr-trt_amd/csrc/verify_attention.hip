@@ -260,8 +260,8 @@ __device__ __forceinline__ void finish_split(const AttnArgs& a, int b, int h, in
 
 // One split's share of row b, head h: tiles sp, sp + nact, sp + 2 nact, ... of the row (r.nact splits).  Leaves
 // the split's unnormalised output rows in ``o`` and its softmax state in ``st``.
-// PIPE: two tiles of registers, the next tile's loads in flight during the current tile's math.
-template <int D, bool PIPE>
+// Two tiles of registers: the next tile's loads are in flight during the current tile's math.
+template <int D>
 __device__ __forceinline__ void attend_split(const AttnArgs& a, int b, int h, int sp, const SplitRange& r,
                                              SoftmaxState& st, f32x4_t (&o)[D / 16], int64_t t0 = 0,
                                              int64_t t1 = -1) {
@@ -316,29 +316,21 @@ __device__ __forceinline__ void attend_split(const AttnArgs& a, int b, int h, in
     attend<D>(t, qop, c_scale, st, o, g, (int)((first + k * r.nact) * 32) + 8 * g, lim_c);
   };
   if (ntot > 0) {
-    KVTile<D> A;
-    if constexpr (PIPE) {
-      KVTile<D> B;
-      load_k(A, 0);
-      int64_t k = 0;
-      for (; k + 2 < ntot; k += 2) {
-        load_k(B, k + 1);
-        attend_k(A, k);
-        load_k(A, k + 2);
-        attend_k(B, k + 1);
-      }
-      if (k + 1 < ntot) {
-        load_k(B, k + 1);
-        attend_k(A, k);
-        attend_k(B, k + 1);
-      } else {
-        attend_k(A, k);
-      }
+    KVTile<D> A, B;
+    load_k(A, 0);
+    int64_t k = 0;
+    for (; k + 2 < ntot; k += 2) {
+      load_k(B, k + 1);
+      attend_k(A, k);
+      load_k(A, k + 2);
+      attend_k(B, k + 1);
+    }
+    if (k + 1 < ntot) {
+      load_k(B, k + 1);
+      attend_k(A, k);
+      attend_k(B, k + 1);
     } else {
-      for (int64_t k = 0; k < ntot; ++k) {
-        load_k(A, k);
-        attend_k(A, k);
-      }
+      attend_k(A, k);
     }
   }
 
@@ -346,8 +338,8 @@ __device__ __forceinline__ void attend_split(const AttnArgs& a, int b, int h, in
 
 // Split-K: one wave per (split, head, row); the split's partial (or, for a row with one split, the output) goes to
 // HBM and a second launch (or the row's last split) merges them.
-template <int D, bool PIPE>
-__global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(AttnArgs a) {
+template <int D>
+__global__ __launch_bounds__(64, 2) void verify_attn_mfma_kernel(AttnArgs a) {
   constexpr int NG = D / 128;
   const int sp = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const SplitRange r = split_range(a, b, sp);
@@ -356,7 +348,7 @@ __global__ __launch_bounds__(64, PIPE ? 2 : 1) void verify_attn_mfma_kernel(Attn
   const int T = a.T;
   SoftmaxState st;
   f32x4_t o[NG * 8];
-  attend_split<D, PIPE>(a, b, h, sp, r, st, o);
+  attend_split<D>(a, b, h, sp, r, st, o);
 
   // ---- finish: per-query sums, then either the output or this split's partial
   float l_tot = st.l_run + __shfl_xor(st.l_run, 16, kWave);
@@ -1181,7 +1173,7 @@ static int launch_attention(const AttnArgs& a, int rows, int dtype, hipStream_t 
   dim3 grid(a.ctx_splits, a.H, rows);
   if (mfma) {
     switch (a.D) {
-      case 128: verify_attn_mfma_kernel<128, true><<<grid, 64, 0, s>>>(a); break;
+      case 128: verify_attn_mfma_kernel<128><<<grid, 64, 0, s>>>(a); break;
       case 256: verify_attn_slice_kernel<256><<<grid, 128, 0, s>>>(a); break;
       case 512: verify_attn_slice_kernel<512><<<grid, 256, 0, s>>>(a); break;
       default: verify_attn_valu_kernel<uint16_t><<<grid, 64, 0, s>>>(a); break;
