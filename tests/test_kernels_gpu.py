@@ -294,6 +294,22 @@ def test_argmax_fp32_and_odd_vocab(cuda, v):
         assert not ((got != want) & ~fragile).any()
 
 
+@pytest.mark.parametrize("v,t", [(32768, 2), (32776, 2), (10288, 64)])
+def test_argmax_launch_boundaries(cuda, v, t):
+    """The row-argmax launch up to 16 chunks per thread (32768 bf16 entries), the one-workgroup-per-slot launch just
+    past it, and the most tokens per row (64): against PyTorch on every row the oracle does not flag."""
+    g = gen(v + t)
+    b = 3
+    x = torch.randn(b * t, v, generator=g).to(torch.bfloat16)
+    xd = x.to(cuda)
+    st = _done_state(cuda, b, t)
+    got = kernels.greedy_accept(xd, st["tokens"], st["out"], st["tok"], st["last"], st["done"], None, None, None,
+                                8188, 2).view(-1).cpu().numpy()
+    want = F.log_softmax(xd, -1).argmax(-1).cpu().numpy()
+    fragile = ov.argmax_is_fragile(npf(x), "bf16")
+    assert not ((got != want) & ~fragile).any()
+
+
 def test_accept_golden_vectors(cuda):
     """The reference's own ``_accept`` outputs (Triton interpreter) on 24 states, through ``omni_accept``."""
     z = np.load(GOLD / "accept_golden.npz")
