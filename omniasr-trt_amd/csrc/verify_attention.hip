@@ -1409,20 +1409,23 @@ __global__ __launch_bounds__(64) void beam_gen_kernel(BeamGenArgs a) {
   }
 }
 
-// The same for bf16 rows of 128 dimensions with both products' loads in one round trip: per pass of up to 64 keys
-// each lane loads its key's K row (16 x 16 bytes) and its share of the V rows (lanes 16g .. 16g + 15 read keys
-// g, g + 4, ..., 8 dimensions each) as soon as the pointers are in, before any score exists.
+// The same for bf16 rows of 128 dimensions, both products' loads in one round trip per 64 keys once the pointers are
+// in, K and V read as whole rows by 16 lanes each (4 rows per load instruction): lane (grp, sub) holds dimensions
+// 8 sub .. 8 sub + 7 of keys grp + 4 ii; its partial dot products are summed over the group's 16 lanes, so every lane
+// of a group holds its 16 keys' scores.  (One lane per key reading its whole K row was 2 us slower at config 5b:
+// 64 rows per load instruction.)
 __global__ __launch_bounds__(64) void beam_gen_kernel_d128(BeamGenArgs a) {
   constexpr int D = 128, kRow = D / 8;  // 16 lanes read a row
-  __shared__ float qs[D];
-  __shared__ float ps[kWave];
-  __shared__ int64_t off_sh[kWave];
-  __shared__ float red[4 * D];
   const int h = blockIdx.x, r = blockIdx.y;
   const int lane = threadIdx.x, grp = lane / kRow, sub = lane - grp * kRow;
   const int64_t n = clamp64(a.gen_len[r], 0, a.gen_cap);
-  const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * a.H + h) * D;
-  for (int d = lane; d < D; d += kWave) qs[d] = bf16_to_f32(qrow[d]) * a.scale_log2;
+  float qv[8];
+  {
+    const u32x4_t q4 =
+        *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * a.H + h) * D + sub * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[e] = bf16x8_elem(q4, e) * a.scale_log2;
+  }
   const char* kb = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(a.kg) + h * a.s_head);
   const char* vb = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(a.vg) + h * a.s_head);
   float m_run = -INFINITY, l_run = 0.f, acc[8];
@@ -1434,50 +1437,62 @@ __global__ __launch_bounds__(64) void beam_gen_kernel_d128(BeamGenArgs a) {
     int64_t src = valid ? (int64_t)a.ptr[(int64_t)r * a.ptr_stride + j] : 0;
     src = clamp64(src, 0, a.gen_rows - 1);
     const int64_t off = (src * a.s_row + (valid ? j : 0) * a.s_pos) * 2;  // bytes; invalid lanes read key 0
-    off_sh[lane] = off;
-    __syncthreads();
-    u32x4_t kx[kRow], vx[kWave / 4];
-#pragma unroll
-    for (int c2 = 0; c2 < kRow; ++c2) kx[c2] = *reinterpret_cast<const u32x4_t*>(kb + off + c2 * 16);
-#pragma unroll
-    for (int ii = 0; ii < kWave / 4; ++ii)
-      vx[ii] = *reinterpret_cast<const u32x4_t*>(vb + off_sh[grp + 4 * ii] + sub * 16);
-    float sc = 0.f;
-#pragma unroll
-    for (int c2 = 0; c2 < kRow; ++c2) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sc = fmaf(qs[c2 * 8 + e], bf16x8_elem(kx[c2], e), sc);
-    }
-    sc = valid ? sc : -INFINITY;
-    const float m_new = fmaxf(m_run, wave_max(sc));
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // m_new is finite: key j0 is valid
-    const float pr = __builtin_amdgcn_exp2f(sc - m_new);
-    l_run = l_run * alpha + pr;
-    m_run = m_new;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] *= alpha;
-    ps[lane] = pr;  // 0 for the invalid keys
-    __syncthreads();
-    const int kend = (int)((n - j0) < kWave ? (n - j0) : kWave);
+    u32x4_t kx[kWave / 4], vx[kWave / 4];
 #pragma unroll
     for (int ii = 0; ii < kWave / 4; ++ii) {
+      const int sl = grp + 4 * ii;
+      const int64_t o2 = (int64_t)(((uint64_t)__shfl((uint32_t)(off >> 32), sl, kWave) << 32) |
+                                   __shfl((uint32_t)off, sl, kWave));
+      kx[ii] = *reinterpret_cast<const u32x4_t*>(kb + o2 + sub * 16);
+      vx[ii] = *reinterpret_cast<const u32x4_t*>(vb + o2 + sub * 16);
+    }
+    const int kend = (int)((n - j0) < kWave ? (n - j0) : kWave);
+    float sc[kWave / 4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int ii = 0; ii < kWave / 4; ++ii) {
+      float part = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part = fmaf(qv[e], bf16x8_elem(kx[ii], e), part);
+#pragma unroll
+      for (int o = 1; o < kRow; o <<= 1) part += __shfl_xor(part, o, kWave);
+      sc[ii] = grp + 4 * ii < kend ? part : -INFINITY;
+      mx = fmaxf(mx, sc[ii]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float m_new = fmaxf(m_run, mx);  // finite: key j0 is valid
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+#pragma unroll
+    for (int ii = 0; ii < kWave / 4; ++ii) {
+      const float p = __builtin_amdgcn_exp2f(sc[ii] - m_new);  // 0 for the keys past the end
+      psum += p;
       const bool kv = grp + 4 * ii < kend;  // rows past the keys in use never reach the product (stale memory)
-      const float p = ps[grp + 4 * ii];
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] = kv ? fmaf(p, bf16x8_elem(vx[ii], e), acc[e]) : acc[e];
     }
-    __syncthreads();
+    psum += __shfl_xor(psum, 16, kWave);
+    psum += __shfl_xor(psum, 32, kWave);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
   }
-  const float l_tot = wave_sum(l_run);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) red[grp * D + sub * 8 + e] = acc[e];
-  __syncthreads();
+  for (int e = 0; e < 8; ++e) {
+    acc[e] += __shfl_xor(acc[e], 16, kWave);
+    acc[e] += __shfl_xor(acc[e], 32, kWave);
+  }
   const int g = r / a.beams, i = r - g * a.beams;
   const int64_t slot = (((int64_t)g * a.H + h) * a.splits + a.gen_split) * a.beams + i;
-  for (int d = lane; d < D; d += kWave) a.part_o[slot * D + d] = red[d] + red[D + d] + red[2 * D + d] + red[3 * D + d];
+  if (grp == 0) {
+    *reinterpret_cast<f32x4_t*>(a.part_o + slot * D + sub * 8) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
+    *reinterpret_cast<f32x4_t*>(a.part_o + slot * D + sub * 8 + 4) = f32x4_t{acc[4], acc[5], acc[6], acc[7]};
+  }
   if (lane == 0) {
     a.part_ml[slot * 2] = m_run;
-    a.part_ml[slot * 2 + 1] = l_tot;
+    a.part_ml[slot * 2 + 1] = l_run;
   }
 }
 
