@@ -370,12 +370,14 @@ def beam_leg(pkg, torch, w: Workload, steps: int, warmup: int, reps: int) -> dic
     return res
 
 
-def time_beam_attention(pkg, torch, reps: int, layers: int = 12, seed: int = 1006) -> dict:
+def time_beam_attention(pkg, torch, reps: int, layers: int = 12, seed: int = 1006, heads: int = 32,
+                        dim: int = 128) -> dict:
     """Config 5b's beam attention without the decoder: 8 inputs x 5 beams, contexts U[750, 2400] and 64 generated
-    keys per row (pointers to random rows), 32 heads x 128, bf16; 12 disjoint cache sets cycled (2.6 GB) so the
-    Infinity Cache cannot serve them; HIP events around graph replays of 24 launches."""
+    keys per row (pointers to random rows), 32 heads x 128 (or ``heads`` x ``dim``), bf16; 12 disjoint cache sets
+    cycled (2.6 GB at 32 x 128) so the Infinity Cache cannot serve them; HIP events around graph replays of 24
+    launches."""
     kernels = pkg.kernels
-    groups, heads, dim, gen, cap, gcap = SLOTS, 32, 128, 64, 2560, 128
+    groups, gen, cap, gcap = SLOTS, 64, 2560, 128
     rows = groups * BEAMS
     rng = np.random.default_rng(seed)
     lengths = rng.integers(750, 2401, groups)
@@ -412,7 +414,8 @@ def time_beam_attention(pkg, torch, reps: int, layers: int = 12, seed: int = 100
     torch.cuda.current_stream().wait_stream(stream)
     us = e0.elapsed_time(e1) * 1000.0 / (reps * 2 * layers)
     nbytes = beam_attention_bytes(lengths, gen, rows, heads, dim)
-    return {"workload": "config 5b beam attention: 8 inputs x 5 beams, contexts U[750, 2400], 64 generated keys",
+    return {"workload": f"config 5b beam attention: 8 inputs x 5 beams, {heads} heads x {dim}, contexts U[750, 2400], "
+                        f"64 generated keys",
             "us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1),
             "frac_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "ctx_keys": ckeys, "launches": reps * 2 * layers}
 
@@ -540,7 +543,7 @@ def main() -> int:
     if args.attention_only and args.beam:
         with torch.inference_mode():
             ref = copy_reference(torch)
-            beam = time_beam_attention(pkg, torch, args.attn_reps)
+            beam = time_beam_attention(pkg, torch, args.attn_reps, heads=args.heads, dim=args.head_dim)
         print(json.dumps({"metric": "beam-attn HBM GB/s (% peak)", "value": beam["GBps"], "unit": "GB/s", "n_gpus": 1,
                           "frac_peak": beam["frac_peak"], "beam_attention": beam, "copy_reference": ref}), flush=True)
         return 0

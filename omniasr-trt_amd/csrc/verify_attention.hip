@@ -1496,6 +1496,108 @@ __global__ __launch_bounds__(64) void beam_gen_kernel_d128(BeamGenArgs a) {
   }
 }
 
+// Generated keys at head dim 512 (bf16, key rows contiguous): a workgroup of 4 waves per (beam row, head), wave w
+// taking keys j0 + 16 w .. j0 + 16 w + 15 of every 64.  Each load instruction reads one whole 1 KB K (or V) row,
+// lane l holding dimensions 8 l .. 8 l + 7, so a wave's 16 keys are one memory round trip once the pointers are in;
+// the partial dot products are summed over the wave, and the 4 waves' (O, m, l) merge in LDS in wave order.
+__global__ __launch_bounds__(256) void beam_gen_kernel_d512(BeamGenArgs a) {
+  constexpr int D = 512, KW = 16, NW = 4;
+  __shared__ float s_o[NW][D];
+  __shared__ float s_m[NW], s_l[NW];
+  const int h = blockIdx.x, r = blockIdx.y;
+  const int tid = threadIdx.x, w = tid / kWave, lane = tid - w * kWave;
+  const int64_t n = clamp64(a.gen_len[r], 0, a.gen_cap);
+  float qv[8];
+  {
+    const u32x4_t q4 =
+        *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)r * a.H + h) * D + lane * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[e] = bf16x8_elem(q4, e) * a.scale_log2;
+  }
+  const char* kb = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(a.kg) + h * a.s_head);
+  const char* vb = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(a.vg) + h * a.s_head);
+  float m_run = -INFINITY, l_run = 0.f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int64_t j0 = 0; j0 < n; j0 += NW * KW) {
+    const int64_t jb = j0 + KW * w;  // this wave's first key
+    const int64_t j = jb + (lane & (KW - 1));
+    const bool valid = j < n;
+    int64_t src = valid ? (int64_t)a.ptr[(int64_t)r * a.ptr_stride + j] : 0;
+    src = clamp64(src, 0, a.gen_rows - 1);
+    const int64_t off = (src * a.s_row + (valid ? j : 0) * a.s_pos) * 2;  // bytes; invalid keys read key 0
+    u32x4_t kx[KW], vx[KW];
+#pragma unroll
+    for (int ii = 0; ii < KW; ++ii) {
+      const int64_t o2 = (int64_t)(((uint64_t)__shfl((uint32_t)(off >> 32), ii, kWave) << 32) |
+                                   __shfl((uint32_t)off, ii, kWave));
+      kx[ii] = *reinterpret_cast<const u32x4_t*>(kb + o2 + lane * 16);
+      vx[ii] = *reinterpret_cast<const u32x4_t*>(vb + o2 + lane * 16);
+    }
+    const int64_t left = n - jb;
+    const int kend = (int)(left < 0 ? 0 : (left < KW ? left : KW));  // this wave's keys in use (wave-uniform)
+    float sc[KW];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int ii = 0; ii < KW; ++ii) {
+      float part = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part = fmaf(qv[e], bf16x8_elem(kx[ii], e), part);
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) part += __shfl_xor(part, o, kWave);
+      sc[ii] = ii < kend ? part : -INFINITY;
+      mx = fmaxf(mx, sc[ii]);
+    }
+    if (kend > 0) {
+      const float m_new = fmaxf(m_run, mx);  // finite: key jb is in use
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      float psum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+#pragma unroll
+      for (int ii = 0; ii < KW; ++ii) {
+        const float p = __builtin_amdgcn_exp2f(sc[ii] - m_new);  // 0 for the keys past the end
+        psum += p;
+        const bool kv = ii < kend;  // rows past the keys in use never reach the product (stale memory)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = kv ? fmaf(p, bf16x8_elem(vx[ii], e), acc[e]) : acc[e];
+      }
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+    }
+  }
+  *reinterpret_cast<f32x4_t*>(&s_o[w][lane * 8]) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
+  *reinterpret_cast<f32x4_t*>(&s_o[w][lane * 8 + 4]) = f32x4_t{acc[4], acc[5], acc[6], acc[7]};
+  if (lane == 0) {
+    s_m[w] = m_run;
+    s_l[w] = l_run;
+  }
+  __syncthreads();
+  if (w != 0) return;
+  float top = s_m[0];
+#pragma unroll
+  for (int q = 1; q < NW; ++q) top = fmaxf(top, s_m[q]);
+  float wt[NW], l_tot = 0.f;
+#pragma unroll
+  for (int q = 0; q < NW; ++q) {
+    wt[q] = s_m[q] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[q] - top);
+    l_tot += wt[q] * s_l[q];
+  }
+  const int g = r / a.beams, i = r - g * a.beams;
+  const int64_t slot = (((int64_t)g * a.H + h) * a.splits + a.gen_split) * a.beams + i;
+#pragma unroll
+  for (int e4 = 0; e4 < 8; e4 += 4) {
+    f32x4_t o4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < NW; ++q) o4 += wt[q] * *reinterpret_cast<const f32x4_t*>(&s_o[q][lane * 8 + e4]);
+    *reinterpret_cast<f32x4_t*>(a.part_o + slot * D + lane * 8 + e4) = o4;
+  }
+  if (lane == 0) {
+    a.part_ml[slot * 2] = top;
+    a.part_ml[slot * 2 + 1] = l_tot;
+  }
+}
+
 }  // namespace omni
 
 extern "C" size_t omni_beam_attention_workspace(int32_t groups, int32_t beams, int32_t heads, int32_t head_dim,
@@ -1594,6 +1696,7 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
   gargs.splits = a.splits;
   gargs.gen_split = a.gen_split;
   if (dtype == OMNI_BF16 && head_dim == 128 && gen_pos == head_dim) beam_gen_kernel_d128<<<ggrid, 64, 0, s>>>(gargs);
+  else if (dtype == OMNI_BF16 && head_dim == 512 && gen_pos == head_dim) beam_gen_kernel_d512<<<ggrid, 256, 0, s>>>(gargs);
   else if (dtype == OMNI_BF16) beam_gen_kernel<uint16_t><<<ggrid, 64, 0, s>>>(gargs);
   else beam_gen_kernel<float><<<ggrid, 64, 0, s>>>(gargs);
   st = omni_launch_status();
