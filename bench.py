@@ -370,6 +370,29 @@ def beam_leg(pkg, torch, w: Workload, steps: int, warmup: int, reps: int) -> dic
     return res
 
 
+def time_prefill_real(pkg, torch, caches, width: int = 2048, reps: int = 3) -> dict:
+    """The causal prefill at the real checkpoint's shape (8 contexts x ``width`` positions x 8 heads x 512, bf16):
+    verify attention over 16-position blocks, one launch pair per context (eager, HIP events)."""
+    kernels = pkg.kernels
+    heads, dim = caches.heads, caches.head_dim
+    g = torch.Generator(device="cuda").manual_seed(1007)
+    q = torch.randn(SLOTS * width, heads, dim, device="cuda", generator=g).to(torch.bfloat16)
+    rows = torch.arange(SLOTS, device="cuda")
+    call = lambda: kernels.prefill_attention(q, caches.k[0], caches.v[0], rows, width, dim ** -0.5)
+    call()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / reps
+    flops = 4 * dim * heads * SLOTS * width * (width + 1) // 2
+    return {"us": round(us, 1), "flops": flops, "TFLOPs": round(flops / us / 1e6, 1),
+            "frac_bf16_peak": round(flops / us / 1e6 / 2500.0, 4)}
+
+
 def time_beam_attention(pkg, torch, reps: int, layers: int = 12, seed: int = 1006, heads: int = 32,
                         dim: int = 128) -> dict:
     """Config 5b's beam attention without the decoder: 8 inputs x 5 beams, contexts U[750, 2400] and 64 generated
@@ -609,6 +632,7 @@ def main() -> int:
         if not args.no_extra:  # the real checkpoint's attention shape: 8 heads x 512 (split-K + merge launch)
             real = AttentionCaches(torch, heads=8, dim=512)
             extra["verify_attention_real_8x8x512"] = time_attention(pkg, torch, real, DRAFT + 1, args.attn_reps)
+            extra["prefill_attention_real_8x2048"] = time_prefill_real(pkg, torch, real)
             del real
         cpu = None
         if not args.no_cpu:

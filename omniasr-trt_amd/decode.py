@@ -140,7 +140,7 @@ class GreedyDecoder:
     def prefill_into(self, ctx: list[Tensor], slots, k_cache: Tensor, v_cache: Tensor) -> Tensor:
         """Contexts into rows ``slots`` of ``k_cache`` / ``v_cache`` ([layers, rows, H, S, Dh]) -- RoPE and the cache
         writes by ``kernels.rope_kv``, causal attention over each context by ``kernels.prefill_attention`` (bf16, head
-        dim 128; fp32 torch attention otherwise); returns the log-softmax after each context's last token [B, V]
+        dim 128, 256 or 512; fp32 torch attention otherwise); returns the log-softmax after each context's last token [B, V]
         (model dtype).  (src/omniasr_trt/decode.py:137-179)"""
         m, b = self.m, len(ctx)
         lens = [c.size(0) for c in ctx]
@@ -159,7 +159,7 @@ class GreedyDecoder:
             qkv = layer.self_attn_layer_norm(h) @ qkv_w.t()
             q = kernels.rope_kv(qkv, m.rope, pos, k_cache[i], v_cache[i], self.heads, slot)
             # Right padding and causal attention: no valid token sees a pad.
-            if fused:  # bf16, head dim 128: the causal HIP kernel over the cache rows just written
+            if fused:  # bf16, head dim 128 / 256 / 512: the HIP causal attention over the cache rows just written
                 o = kernels.prefill_attention(q, k_cache[i], v_cache[i], ctx_rows, width, self.head_dim ** -0.5)
                 o = o.view(b * width, -1)
             else:  # fp32 math keeps bf16 batched products (and their transposed operands) out of this path

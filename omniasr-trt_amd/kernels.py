@@ -215,10 +215,11 @@ def beam_attention(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, ctx_len:
 
 def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, slots: torch.Tensor,
                       width: int, scale: float) -> torch.Tensor:
-    """Causal attention of whole contexts over their cache rows: ``q`` [B*width, H, 128] bf16 (context b's queries
-    at rows b*width ..), ``k_cache``/``v_cache`` [rows, H, S >= width, 128] bf16 with unit stride in D, ``slots`` [B]
+    """Causal attention of whole contexts over their cache rows: ``q`` [B*width, H, D] bf16, D = 128 (the causal kernel)
+    or 256 / 512 (see :func:`_prefill_by_blocks`) (context b's queries at rows b*width ..), ``k_cache``/``v_cache``
+    [rows, H, S >= width, D] bf16 with unit stride in D, ``slots`` [B]
     the contexts' cache rows; query p of context b attends to keys [0, p] of row ``slots[b]``.  Returns
-    [B*width, H, 128] -- ``F.scaled_dot_product_attention(q, k, v, is_causal=True)`` of the prefill
+    [B*width, H, D] -- ``F.scaled_dot_product_attention(q, k, v, is_causal=True)`` of the prefill
     (src/omniasr_trt/decode.py:163-164), in the query layout of :func:`rope_kv`."""
     lib = _lib.load()
     rows, heads, dim = q.shape
@@ -232,6 +233,8 @@ def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
     _need(k_cache.size(2) >= width, "caches: at least width positions")
     _index(slots, "slots")
     _need(slots.numel() >= contexts, "slots: [B]")
+    if dim in (256, 512) and q.dtype == torch.bfloat16:
+        return _prefill_by_blocks(q, k_cache, v_cache, slots, width, scale)
     out = torch.empty_like(q)
     status = lib.omni_prefill_attention(
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
@@ -241,9 +244,34 @@ def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
     return out
 
 
+def _prefill_by_blocks(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, slots: torch.Tensor,
+                       width: int, scale: float) -> torch.Tensor:
+    """Head dims 256 / 512: the causal prefill as verify attention over blocks of 16 positions.  Block j of a context
+    is a verify row whose 16 queries are positions 16j .. 16j + 15 with ``lengths = 16j + 1``, so query i sees keys
+    [0, 16j + i] -- the causal mask; every block of a context reads the context's cache row (row stride 0).  One
+    launch per context (the cache rows are read on the host); positions past the width are computed on zero
+    queries and dropped."""
+    rows, heads, dim = q.shape
+    contexts = rows // width
+    blocks = -(-width // 16)
+    padded = blocks * 16
+    lengths = torch.arange(0, padded, 16, device=q.device, dtype=torch.long) + 1
+    keys = min(-(-padded // 256) * 256, k_cache.size(2))
+    out = torch.empty_like(q)
+    qb = torch.zeros(padded, heads, dim, device=q.device, dtype=q.dtype)
+    for b, row in enumerate(slots[:contexts].tolist()):
+        qb[:width] = q[b * width:(b + 1) * width]
+        kc = k_cache[row].unsqueeze(0).expand(blocks, -1, -1, -1)
+        vc = v_cache[row].unsqueeze(0).expand(blocks, -1, -1, -1)
+        o = _verify(qb, kc, vc, lengths, 16, keys, scale, 0, True)
+        out[b * width:(b + 1) * width] = o[:width]
+    return out
+
+
 def prefill_supported(dtype: torch.dtype, head_dim: int) -> bool:
-    """Whether :func:`prefill_attention` covers this element type and head size (bf16, 128)."""
-    return dtype == torch.bfloat16 and head_dim == 128
+    """Whether :func:`prefill_attention` covers this element type and head size: bf16 with head dim 128 (the causal
+    kernel) or 256 / 512 (verify attention over 16-position blocks)."""
+    return dtype == torch.bfloat16 and head_dim in (128, 256, 512)
 
 
 def splits_for(rows: int, heads: int, keys: int, block: int = 64, programs: int = 264) -> tuple[int, int]:

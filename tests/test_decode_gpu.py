@@ -155,21 +155,23 @@ def test_graph_replays_equal_eager_steps(cuda):
     assert a.stats["rows_steps"] == b.stats["rows_steps"] and a.stats["captures"] > 0
 
 
-def test_bf16_prefill_kernel_matches_torch_attention(cuda, monkeypatch):
-    """A bf16 model with head dim 128: the prefill through kernels.prefill_attention gives the log-probabilities of
-    the fp32 torch attention path within bf16 tolerance, for contexts of different lengths in permuted cache rows."""
+@pytest.mark.parametrize("model_dim,heads", [(256, 2), (512, 1)])
+def test_bf16_prefill_kernel_matches_torch_attention(cuda, monkeypatch, model_dim, heads):
+    """A bf16 model with head dim 128 (the causal kernel) or 512 (16-position verify blocks): the prefill through
+    kernels.prefill_attention gives the log-probabilities of the fp32 torch attention path within bf16 tolerance,
+    for contexts of different lengths in permuted cache rows."""
     torch.manual_seed(31)
-    cfg = DecoderConfig(model_dim=256, num_layers=2, num_heads=2, ffn_dim=64, vocab_size=40, num_langs=5)
+    cfg = DecoderConfig(model_dim=model_dim, num_layers=2, num_heads=heads, ffn_dim=64, vocab_size=40, num_langs=5)
     m = DecoderModel(cfg).eval()
     with torch.no_grad():
         for p in m.parameters():
             p.normal_(0, 0.05)
     m = m.to(torch.bfloat16).cuda()
     dec = GreedyDecoder(m, max_batch=3, graphs=False, reserve=8)
-    ctxs = [torch.randn(n, 256).to(torch.bfloat16).cuda() for n in (70, 5, 133)]
+    ctxs = [torch.randn(n, model_dim).to(torch.bfloat16).cuda() for n in (70, 5, 133)]
 
     def prefill():
-        k = torch.zeros(2, 4, 2, 160, 128, dtype=torch.bfloat16, device=cuda)
+        k = torch.zeros(2, 4, heads, 160, model_dim // heads, dtype=torch.bfloat16, device=cuda)
         v = torch.zeros_like(k)
         logp = dec.prefill_into(ctxs, [3, 0, 2], k, v)
         torch.cuda.synchronize()

@@ -118,18 +118,19 @@ def test_verify_attention_bf16(cuda, t):
     _attn_case(cuda, torch.bfloat16, 4, 4, 256, t, 700, lengths, 640, 5, BF16_TOL)  # two 128-dimension slices
 
 
-@pytest.mark.parametrize("width", [1, 15, 64, 97, 300])
-def test_prefill_attention(cuda, width):
+@pytest.mark.parametrize("width,d", [(1, 128), (15, 128), (64, 128), (97, 128), (300, 128), (15, 512), (97, 512),
+                                     (300, 256)])
+def test_prefill_attention(cuda, width, d):
     """Causal attention over whole contexts (src/omniasr_trt/decode.py:163-164) against the oracle's verify attention
     with query p of a context over keys [0, p]: cache rows addressed through slots, widths that are not multiples
-    of the 192-query block or the 32-key tile."""
+    of the 192-query block or the 32-key tile; head dims 256 / 512 through 16-position verify blocks."""
     g = gen(60 + width)
-    b, h, d, rows, cap = 3, 4, 128, 5, 320
+    b, h, rows, cap = 3, 4, 5, 320
     kc = torch.randn(rows, h, cap, d, generator=g).to(torch.bfloat16)
     vc = torch.randn(rows, h, cap, d, generator=g).to(torch.bfloat16)
     q = torch.randn(b * width, h, d, generator=g).to(torch.bfloat16)
     slots = torch.tensor([4, 0, 2])
-    say(f"prefill attention width={width}")
+    say(f"prefill attention width={width} d={d}")
     out = kernels.prefill_attention(q.to(cuda), kc.to(cuda), vc.to(cuda), slots.to(cuda), width, d ** -0.5)
     torch.cuda.synchronize()
     sl = slots.numpy()
