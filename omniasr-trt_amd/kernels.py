@@ -10,15 +10,18 @@ through its C ABI (``include/omniasr_mi355x.h``) on torch's current stream:
   keys, causal among the new ones, one read of the keys for all of them; :func:`decode_attention` is
   its one-query case (``omni_verify_attention``);
 * :func:`propose` -- the draft proposal of every row (``omni_propose``);
-* :func:`accept` -- greedy acceptance and rollback (``omni_accept``).
+* :func:`accept` -- greedy acceptance and rollback (``omni_accept``);
+* :func:`beam_attention` -- beam search's shared-context plus generated-keys attention (``omni_beam_attention``).
 
 Beyond the reference's functions, for the fused step: :func:`spec_prepare` (proposal plus the step's
 tokens / positions / cache rows / key counts in one launch) and :func:`greedy_accept` (the argmax of
-the verify logits and the acceptance).
+the verify logits and the acceptance); for the prefill: :func:`prefill_attention` (causal attention of whole
+contexts, the reference's ``F.scaled_dot_product_attention(is_causal=True)``).
 
 Nothing here synchronises or allocates beyond the outputs and the attention workspace (from torch's
-allocator, so from a graph's pool under capture), so every function can be captured in a HIP graph.
-There is no other code path: on a GPU without the library these functions raise.
+allocator, so from a graph's pool under capture), so every function can be captured in a HIP graph -- except
+:func:`prefill_attention` at head dims 256 / 512, which reads the contexts' cache rows on the host (the decoders
+run the prefill eagerly).  There is no other code path: on a GPU without the library these functions raise.
 """
 
 from __future__ import annotations
