@@ -411,7 +411,7 @@ extern "C" int omni_greedy_accept(const void* logits, int64_t logits_stride, int
   // Argmax by row, then the acceptance (when the argmaxes have somewhere to go and a row fits 16 chunks per
   // thread of a 256-thread workgroup: vocabularies up to 32768 bf16 / 16384 fp32 entries).
   const int64_t rkpt = (nchunks + kRowThreads - 1) / kRowThreads;
-  if (nxt && rkpt <= 16) {
+  if (nxt && rkpt <= 16 && (int64_t)rows * tokens_per_row <= INT_MAX) {  // the grid has one workgroup per row
     const int rk = rkpt <= 1 ? 1 : rkpt <= 2 ? 2 : rkpt <= 4 ? 4 : rkpt <= 8 ? 8 : 16;
     const int nrows = rows * tokens_per_row;
 #define OMNI_ROW_ARGMAX(L, K)                                                       \
