@@ -32,9 +32,9 @@ struct RopeVec<uint16_t> {  // bf16: 8 elements = 4 pairs in 16 bytes
     for (int w = 0; w < 4; ++w) v[w] = pack_bf16x2(f[2 * w], f[2 * w + 1]);
     *reinterpret_cast<u32x4_t*>(p) = v;
   }
-  __device__ static void copy(const uint16_t* src, uint16_t* dst) {
-    *reinterpret_cast<u32x4_t*>(dst) = *reinterpret_cast<const u32x4_t*>(src);
-  }
+  typedef u32x4_t Raw;  // 16 bytes moved as they are
+  __device__ static Raw raw(const uint16_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
+  __device__ static void store_raw(uint16_t* p, Raw v) { *reinterpret_cast<u32x4_t*>(p) = v; }
 };
 
 template <>
@@ -51,9 +51,9 @@ struct RopeVec<float> {  // fp32: 4 elements = 2 pairs in 16 bytes
     for (int e = 0; e < 4; ++e) v[e] = f[e];
     *reinterpret_cast<f32x4_t*>(p) = v;
   }
-  __device__ static void copy(const float* src, float* dst) {
-    *reinterpret_cast<f32x4_t*>(dst) = *reinterpret_cast<const f32x4_t*>(src);
-  }
+  typedef u32x4_t Raw;
+  __device__ static Raw raw(const float* p) { return *reinterpret_cast<const u32x4_t*>(p); }
+  __device__ static void store_raw(float* p, Raw v) { *reinterpret_cast<u32x4_t*>(p) = v; }
 };
 
 // (re, im) -> (re*c - im*s, re*s + im*c), every operation rounded separately.
@@ -84,7 +84,17 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(
   const int h = piece / per_head;
   const int e0 = (piece - h * per_head) * kE;  // first element of this thread's 16 bytes
 
+  // Every load that does not depend on a loaded value is issued first (the token's q, k and v, its position, cache
+  // row and cache position); only the cos / sin row waits for the position.
+  const Elem* row = qkv + n * qkv_row_stride + (int64_t)h * head_dim + e0;
+  const int64_t hd = (int64_t)heads * head_dim;
+  float xq[kE], xk[kE];
+  V::load(row, xq);
+  V::load(row + hd, xk);
+  typename V::Raw vraw = V::raw(row + 2 * hd);
   const int64_t p = pos[n];
+  const int64_t r = slots ? slots[n] : n;
+  const int64_t cp = cache_pos ? cache_pos[n] : p;
   const int64_t pt = clamp64(p, 0, cs_rows - 1);  // table row (valid positions never clamp)
   // cs[p] holds (c, s) of pair j at floats 2j, 2j+1: this thread's pairs are floats e0 .. e0+kE-1.
   const f32x4_t* csr = reinterpret_cast<const f32x4_t*>(cs + pt * head_dim + e0);
@@ -98,28 +108,22 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(
     s[2 * w + 1] = t[3];
   }
 
-  const Elem* row = qkv + n * qkv_row_stride + (int64_t)h * head_dim + e0;
-  const int64_t hd = (int64_t)heads * head_dim;
-  float x[kE], y[kE];
+  float y[kE];
 
   // q
-  V::load(row, x);
 #pragma unroll
-  for (int j = 0; j < kE / 2; ++j) rotate_pair(x[2 * j], x[2 * j + 1], c[j], s[j], y[2 * j], y[2 * j + 1]);
+  for (int j = 0; j < kE / 2; ++j) rotate_pair(xq[2 * j], xq[2 * j + 1], c[j], s[j], y[2 * j], y[2 * j + 1]);
   V::store(q_out + (n * heads + h) * (int64_t)head_dim + e0, y);
 
-  const int64_t r = slots ? slots[n] : n;
-  const int64_t cp = cache_pos ? cache_pos[n] : p;
   if (r < 0 || r >= cache_rows || cp < 0 || cp >= cache_len) return;  // outside the cache: no write
   const int64_t off = r * stride_row + (int64_t)h * stride_head + cp * stride_pos + e0;
 
   // k
-  V::load(row + hd, x);
 #pragma unroll
-  for (int j = 0; j < kE / 2; ++j) rotate_pair(x[2 * j], x[2 * j + 1], c[j], s[j], y[2 * j], y[2 * j + 1]);
+  for (int j = 0; j < kE / 2; ++j) rotate_pair(xk[2 * j], xk[2 * j + 1], c[j], s[j], y[2 * j], y[2 * j + 1]);
   V::store(k_cache + off, y);
   // v: copied as it is
-  V::copy(row + 2 * hd, v_cache + off);
+  V::store_raw(v_cache + off, vraw);
 }
 
 }  // namespace omni
