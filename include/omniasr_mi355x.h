@@ -104,7 +104,7 @@ size_t omni_verify_attention_workspace(int32_t rows, int32_t tokens, int32_t hea
  * timing).  Otherwise, or when ``flags`` has OMNI_ATTN_SPLIT_K, split-K as above.
  * bf16: head_dim 128, 256 or 512 with contiguous key rows runs on MFMA (256 / 512: a workgroup of one wave per
  * 128 dimensions, the partial scores added through LDS), any other multiple of 8 on the vector ALUs; f32:
- * vector ALUs (fp32 products).  tokens: 1..16.
+ * vector ALUs (fp32 products).  tokens: 1..16 (1..32 for bf16 head dims 256 / 512 with contiguous key rows).
  */
 int omni_verify_attention(const void *q, const void *k_cache, const void *v_cache,
                           int64_t stride_row, int64_t stride_head, int64_t stride_pos,

@@ -406,10 +406,10 @@ __global__ __launch_bounds__(64, 2) void verify_attn_mfma_kernel(AttnArgs a) {
 // and after one barrier every wave adds the D/128 partials in slice order, so all waves hold the same scores and
 // the same softmax state; each then accumulates its own slice of P V.  Tiles are dealt to the splits as in
 // attend_split; the partials and the last split's merge are those of verify_attn_mfma_kernel.
-template <int D>
-__global__ __launch_bounds__(64 * (D / 128), 2) void verify_attn_slice_kernel(AttnArgs a) {
+template <int D, int G>
+__global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_slice_kernel(AttnArgs a) {
   constexpr int NSL = D / 128;
-  __shared__ float sx[2][NSL][kWave * 8];  // partial scores of a tile by slice, double-buffered
+  __shared__ float sx[2][NSL][G][kWave * 8];  // partial scores of a tile by slice and query group, double-buffered
   __shared__ int s_ticket;
   const int sp = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const SplitRange r = split_range(a, b, sp);
@@ -417,18 +417,26 @@ __global__ __launch_bounds__(64 * (D / 128), 2) void verify_attn_slice_kernel(At
   const int lane = lane_id(), w = threadIdx.x / kWave, c = lane & 15, g = lane >> 4;
   const int T = a.T;
 
-  u32x4_t qop[4];  // B operand of the slice's S^T = K Q^T: lane (c, g) holds q[c][128w + 32s + 8g .. + 7]
-  {
+  // Query group u holds queries 16u .. 16u + 15 of the row.  B operand of the slice's S^T = K Q^T: lane (c, g) holds
+  // q[16u + c][128w + 32s + 8g .. + 7].
+  u32x4_t qop[G][4];
+  SoftmaxState st[G];
+  f32x4_t o[G][8];
+  int lim_c[G];
+#pragma unroll
+  for (int u = 0; u < G; ++u) {
+    const int qi = 16 * u + c;
     const uint16_t* qrow =
-        reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)(b * T + c) * a.H + h) * D + w * 128 + g * 8;
+        reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)(b * T + qi) * a.H + h) * D + w * 128 + g * 8;
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2)
-      qop[s2] = c < T ? *reinterpret_cast<const u32x4_t*>(qrow + s2 * 32) : u32x4_t{0u, 0u, 0u, 0u};
-  }
-  SoftmaxState st{-INFINITY, -INFINITY, 0.f};
-  f32x4_t o[8];
+      qop[u][s2] = qi < T ? *reinterpret_cast<const u32x4_t*>(qrow + s2 * 32) : u32x4_t{0u, 0u, 0u, 0u};
+    st[u] = SoftmaxState{-INFINITY, -INFINITY, 0.f};
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int nb = 0; nb < 8; ++nb) o[u][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int64_t own = r.n + (a.causal ? qi : 0);
+    lim_c[u] = (int)(own < r.total ? own : r.total);
+  }
 
   const int64_t row_tiles = (r.total + 31) >> 5;
   const int64_t first = sp;
@@ -438,8 +446,6 @@ __global__ __launch_bounds__(64 * (D / 128), 2) void verify_attn_slice_kernel(At
   const char* vt = reinterpret_cast<const char*>(a.v) + (b * a.s_row + h * a.s_head + first * 32 * D) * 2 + w * 256;
   const int64_t tile_bytes = (int64_t)r.nact * 32 * D * 2;
   const int64_t last_key = a.cache_len - 1;
-  const int64_t own = r.n + (a.causal ? c : 0);
-  const int lim_c = (int)(own < r.total ? own : r.total);
   auto load_k = [&](KVTile<128>& t, int64_t k) {
     const int64_t kb = (first + k * r.nact) * 32;
     const int64_t kmax = last_key - kb, vstop = r.total - kb;
@@ -447,24 +453,30 @@ __global__ __launch_bounds__(64 * (D / 128), 2) void verify_attn_slice_kernel(At
                                   vstop < 32 ? (int)vstop : 32, c, g);
   };
   auto attend_k = [&](const KVTile<128>& t, int64_t k) {
-    float sv[8];
-    tile_scores<128>(t, qop, sv);
-    float* mine = &sx[k & 1][w][lane * 8];
-    *reinterpret_cast<f32x4_t*>(mine) = f32x4_t{sv[0], sv[1], sv[2], sv[3]};
-    *reinterpret_cast<f32x4_t*>(mine + 4) = f32x4_t{sv[4], sv[5], sv[6], sv[7]};
-    lds_barrier();
-    float tot[8];
 #pragma unroll
-    for (int ww = 0; ww < NSL; ++ww) {
-      const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(&sx[k & 1][ww][lane * 8]);
-      const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(&sx[k & 1][ww][lane * 8 + 4]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        tot[j] = ww == 0 ? lo[j] : tot[j] + lo[j];
-        tot[j + 4] = ww == 0 ? hi[j] : tot[j + 4] + hi[j];
-      }
+    for (int u = 0; u < G; ++u) {
+      float sv[8];
+      tile_scores<128>(t, qop[u], sv);
+      float* mine = &sx[k & 1][w][u][lane * 8];
+      *reinterpret_cast<f32x4_t*>(mine) = f32x4_t{sv[0], sv[1], sv[2], sv[3]};
+      *reinterpret_cast<f32x4_t*>(mine + 4) = f32x4_t{sv[4], sv[5], sv[6], sv[7]};
     }
-    attend_scored<128>(t, tot, a.scale_log2, st, o, g, (int)((first + k * r.nact) * 32) + 8 * g, lim_c);
+    lds_barrier();
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      float tot[8];
+#pragma unroll
+      for (int ww = 0; ww < NSL; ++ww) {
+        const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(&sx[k & 1][ww][u][lane * 8]);
+        const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(&sx[k & 1][ww][u][lane * 8 + 4]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          tot[j] = ww == 0 ? lo[j] : tot[j] + lo[j];
+          tot[j + 4] = ww == 0 ? hi[j] : tot[j + 4] + hi[j];
+        }
+      }
+      attend_scored<128>(t, tot, a.scale_log2, st[u], o[u], g, (int)((first + k * r.nact) * 32) + 8 * g, lim_c[u]);
+    }
   };
   // The buffer written for tile k was last read for tile k - 2, before every wave passed tile k - 1's barrier.
   if (ntot > 0) {
@@ -487,50 +499,55 @@ __global__ __launch_bounds__(64 * (D / 128), 2) void verify_attn_slice_kernel(At
   }
 
   // ---- finish: per-query sums (the same in every wave), then the output slice or this split's partial slice
-  float l_tot = st.l_run + __shfl_xor(st.l_run, 16, kWave);
-  l_tot += __shfl_xor(l_tot, 32, kWave);
-  float li[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) li[i] = __shfl(l_tot, 4 * g + i, kWave);
-  if (r.nact == 1 && a.gen_split < 0) {
-    uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 4 * g + i;
-      if (t >= T) continue;
-      const float div = li[i] > 0.f ? li[i] : 1.f;
-      u32x4_t wv;
-#pragma unroll
-      for (int q2 = 0; q2 < 4; ++q2) wv[q2] = pack_bf16x2(o[2 * q2][i] / div, o[2 * q2 + 1][i] / div);
-      *reinterpret_cast<u32x4_t*>(out + ((int64_t)(b * T + t) * a.H + h) * D + w * 128 + c * 8) = wv;
-    }
-    return;
-  }
+  const bool direct = r.nact == 1 && a.gen_split < 0;
   const int64_t base = (((int64_t)b * a.H + h) * a.splits + sp) * T;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = 4 * g + i;
-    if (t >= T) continue;
-    float* po = a.part_o + (base + t) * D + w * 128 + c * 8;
-    const f32x4_t x0 = f32x4_t{o[0][i], o[1][i], o[2][i], o[3][i]};
-    const f32x4_t x1 = f32x4_t{o[4][i], o[5][i], o[6][i], o[7][i]};
-    if (a.separate) {
-      reinterpret_cast<f32x4_t*>(po)[0] = x0;
-      reinterpret_cast<f32x4_t*>(po)[1] = x1;
-    } else {
-      put_through4c(po, x0);
-      put_through4c(po + 4, x1);
+  for (int u = 0; u < G; ++u) {
+    float l_tot = st[u].l_run + __shfl_xor(st[u].l_run, 16, kWave);
+    l_tot += __shfl_xor(l_tot, 32, kWave);
+    float li[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) li[i] = __shfl(l_tot, 4 * g + i, kWave);
+    if (direct) {
+      uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * u + 4 * g + i;
+        if (t >= T) continue;
+        const float div = li[i] > 0.f ? li[i] : 1.f;
+        u32x4_t wv;
+#pragma unroll
+        for (int q2 = 0; q2 < 4; ++q2) wv[q2] = pack_bf16x2(o[u][2 * q2][i] / div, o[u][2 * q2 + 1][i] / div);
+        *reinterpret_cast<u32x4_t*>(out + ((int64_t)(b * T + t) * a.H + h) * D + w * 128 + c * 8) = wv;
+      }
+      continue;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * u + 4 * g + i;
+      if (t >= T) continue;
+      float* po = a.part_o + (base + t) * D + w * 128 + c * 8;
+      const f32x4_t x0 = f32x4_t{o[u][0][i], o[u][1][i], o[u][2][i], o[u][3][i]};
+      const f32x4_t x1 = f32x4_t{o[u][4][i], o[u][5][i], o[u][6][i], o[u][7][i]};
+      if (a.separate) {
+        reinterpret_cast<f32x4_t*>(po)[0] = x0;
+        reinterpret_cast<f32x4_t*>(po)[1] = x1;
+      } else {
+        put_through4c(po, x0);
+        put_through4c(po + 4, x1);
+      }
+    }
+    const int tc = 16 * u + c;
+    if (w == 0 && g == 0 && tc < T) {
+      if (a.separate) {
+        a.part_ml[(base + tc) * 2] = st[u].m_ref;
+        a.part_ml[(base + tc) * 2 + 1] = l_tot;
+      } else {
+        put_through2(a.part_ml + (base + tc) * 2, st[u].m_ref, l_tot);
+      }
     }
   }
-  if (w == 0 && g == 0 && c < T) {
-    if (a.separate) {
-      a.part_ml[(base + c) * 2] = st.m_ref;
-      a.part_ml[(base + c) * 2 + 1] = l_tot;
-    } else {
-      put_through2(a.part_ml + (base + c) * 2, st.m_ref, l_tot);
-    }
-  }
-  if (a.separate) return;
+  if (direct || a.separate) return;
   // Every wave's partial stores have reached the coherence point before the split's ticket is taken.
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);
@@ -1174,8 +1191,14 @@ static int launch_attention(const AttnArgs& a, int rows, int dtype, hipStream_t 
   if (mfma) {
     switch (a.D) {
       case 128: verify_attn_mfma_kernel<128><<<grid, 64, 0, s>>>(a); break;
-      case 256: verify_attn_slice_kernel<256><<<grid, 128, 0, s>>>(a); break;
-      case 512: verify_attn_slice_kernel<512><<<grid, 256, 0, s>>>(a); break;
+      case 256:
+        if (a.T > 16) verify_attn_slice_kernel<256, 2><<<grid, 128, 0, s>>>(a);
+        else verify_attn_slice_kernel<256, 1><<<grid, 128, 0, s>>>(a);
+        break;
+      case 512:
+        if (a.T > 16) verify_attn_slice_kernel<512, 2><<<grid, 256, 0, s>>>(a);
+        else verify_attn_slice_kernel<512, 1><<<grid, 256, 0, s>>>(a);
+        break;
       default: verify_attn_valu_kernel<uint16_t><<<grid, 64, 0, s>>>(a); break;
     }
   } else if (dtype == OMNI_BF16) {
@@ -1205,10 +1228,13 @@ static int launch_combine(const AttnArgs& a, int rows, int dtype, hipStream_t s)
   return omni_launch_status();
 }
 
-static int check_attention_shape(int32_t tokens, int32_t heads, int32_t head_dim, int32_t dtype, float scale) {
+static int check_attention_shape(int32_t tokens, int32_t heads, int32_t head_dim, int32_t dtype, float scale,
+                                 int64_t stride_pos) {
   if (heads <= 0 || head_dim <= 0) return OMNI_ERR_INVALID;
   if (!(scale > 0.f)) return OMNI_ERR_INVALID;  // a softmax scale is positive (head_dim^-1/2)
-  if (tokens < 1 || tokens > 16) return OMNI_ERR_SHAPE;
+  // Up to 16 queries per row; up to 32 on the wide-head MFMA kernel (two query groups per wave).
+  const bool wide = dtype == OMNI_BF16 && (head_dim == 256 || head_dim == 512) && stride_pos == head_dim;
+  if (tokens < 1 || tokens > (wide ? 32 : 16)) return OMNI_ERR_SHAPE;
   if (dtype != OMNI_BF16 && dtype != OMNI_F32) return OMNI_ERR_DTYPE;
   if (head_dim % 8 != 0 || head_dim > kValuMaxD) return OMNI_ERR_SHAPE;
   return OMNI_OK;
@@ -1233,7 +1259,7 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
                                      size_t workspace_bytes, int32_t* counters, int32_t flags,
                                      int32_t dtype, void* stream) {
   if (rows < 0 || keys <= 0 || cache_len <= 0) return OMNI_ERR_INVALID;
-  int st = check_attention_shape(tokens, heads, head_dim, dtype, scale);
+  int st = check_attention_shape(tokens, heads, head_dim, dtype, scale, stride_pos);
   if (st != OMNI_OK) return st;
   if (rows == 0) return OMNI_OK;
   if (!q || !k_cache || !v_cache || !lengths || !out || !workspace || !counters) return OMNI_ERR_INVALID;
@@ -1619,7 +1645,7 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
                                    void* out, void* workspace, size_t workspace_bytes, int32_t* counters,
                                    int32_t dtype, void* stream) {
   if (groups < 0 || ctx_keys <= 0 || ctx_cap <= 0 || gen_cap <= 0 || gen_rows <= 0) return OMNI_ERR_INVALID;
-  int st = check_attention_shape(beams, heads, head_dim, dtype, scale);
+  int st = check_attention_shape(beams, heads, head_dim, dtype, scale, 0);  // beams: 1..16
   if (st != OMNI_OK) return st;
   if (groups == 0) return OMNI_OK;
   if (!q || !k_ctx || !v_ctx || !ctx_len || !k_gen || !v_gen || !ptr || !gen_len || !out || !workspace)

@@ -249,16 +249,17 @@ def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
 
 def _prefill_by_blocks(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, slots: torch.Tensor,
                        width: int, scale: float) -> torch.Tensor:
-    """Head dims 256 / 512: the causal prefill as verify attention over blocks of 16 positions.  Block j of a context
-    is a verify row whose 16 queries are positions 16j .. 16j + 15 with ``lengths = 16j + 1``, so query i sees keys
-    [0, 16j + i] -- the causal mask; every block of a context reads the context's cache row (row stride 0).  One
+    """Head dims 256 / 512: the causal prefill as verify attention over blocks of 32 positions.  Block j of a context
+    is a verify row whose 32 queries are positions 32j .. 32j + 31 with ``lengths = 32j + 1``, so query i sees keys
+    [0, 32j + i] -- the causal mask; every block of a context reads the context's cache row (row stride 0).  One
     launch per context (the cache rows are read on the host); positions past the width are computed on zero
     queries and dropped."""
     rows, heads, dim = q.shape
     contexts = rows // width
-    blocks = -(-width // 16)
-    padded = blocks * 16
-    lengths = torch.arange(0, padded, 16, device=q.device, dtype=torch.long) + 1
+    blk = 32  # positions per block: two 16-query groups per wave
+    blocks = -(-width // blk)
+    padded = blocks * blk
+    lengths = torch.arange(0, padded, blk, device=q.device, dtype=torch.long) + 1
     keys = min(-(-padded // 256) * 256, k_cache.size(2))
     out = torch.empty_like(q)
     qb = torch.zeros(padded, heads, dim, device=q.device, dtype=q.dtype)
@@ -266,7 +267,7 @@ def _prefill_by_blocks(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
         qb[:width] = q[b * width:(b + 1) * width]
         kc = k_cache[row].unsqueeze(0).expand(blocks, -1, -1, -1)
         vc = v_cache[row].unsqueeze(0).expand(blocks, -1, -1, -1)
-        o = _verify(qb, kc, vc, lengths, 16, keys, scale, 0, True)
+        o = _verify(qb, kc, vc, lengths, blk, keys, scale, 0, True)
         out[b * width:(b + 1) * width] = o[:width]
     return out
 

@@ -118,6 +118,20 @@ def test_verify_attention_bf16(cuda, t):
     _attn_case(cuda, torch.bfloat16, 4, 4, 256, t, 700, lengths, 640, 5, BF16_TOL)  # two 128-dimension slices
 
 
+@pytest.mark.parametrize("t,d", [(20, 512), (32, 512), (32, 256)])
+def test_verify_attention_wide_heads_up_to_32_queries(cuda, t, d):
+    """Head dims 256 / 512 take up to 32 queries per row (two 16-query groups per wave): against the oracle, both
+    merge modes; a 128-wide head with more than 16 queries is refused."""
+    lengths = torch.tensor([600, 257, 1, 0])
+    a = _attn_case(cuda, torch.bfloat16, 4, 2, d, t, 700, lengths, 640, 11, BF16_TOL, separate=True)
+    b = _attn_case(cuda, torch.bfloat16, 4, 2, d, t, 700, lengths, 640, 11, BF16_TOL, separate=False)
+    torch.testing.assert_close(a.float(), b.float(), atol=1e-2, rtol=1e-2)
+    q = torch.zeros(2 * 17, 2, 128, dtype=torch.bfloat16, device=cuda)
+    kc = torch.zeros(2, 2, 256, 128, dtype=torch.bfloat16, device=cuda)
+    with pytest.raises(RuntimeError):
+        kernels.draft_attention(q, kc, kc, torch.tensor([5, 9], device=cuda), 17, 256, 0.1)
+
+
 @pytest.mark.parametrize("width,d", [(1, 128), (15, 128), (64, 128), (97, 128), (300, 128), (15, 512), (97, 512),
                                      (300, 256)])
 def test_prefill_attention(cuda, width, d):
