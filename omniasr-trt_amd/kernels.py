@@ -274,7 +274,7 @@ def _prefill_by_blocks(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
 
 def prefill_supported(dtype: torch.dtype, head_dim: int) -> bool:
     """Whether :func:`prefill_attention` covers this element type and head size: bf16 with head dim 128 (the causal
-    kernel) or 256 / 512 (verify attention over 16-position blocks)."""
+    kernel) or 256 / 512 (verify attention over 32-position blocks)."""
     return dtype == torch.bfloat16 and head_dim in (128, 256, 512)
 
 

@@ -137,7 +137,7 @@ def test_verify_attention_wide_heads_up_to_32_queries(cuda, t, d):
 def test_prefill_attention(cuda, width, d):
     """Causal attention over whole contexts (src/omniasr_trt/decode.py:163-164) against the oracle's verify attention
     with query p of a context over keys [0, p]: cache rows addressed through slots, widths that are not multiples
-    of the 192-query block or the 32-key tile; head dims 256 / 512 through 16-position verify blocks."""
+    of the 192-query block or the 32-key tile; head dims 256 / 512 through 32-position verify blocks."""
     g = gen(60 + width)
     b, h, rows, cap = 3, 4, 5, 320
     kc = torch.randn(rows, h, cap, d, generator=g).to(torch.bfloat16)
