@@ -59,3 +59,16 @@ def test_decoders_refuse_a_cpu_model():
         decode.GreedyDecoder(modeling.DecoderModel(cfg))
     with pytest.raises(ValueError):
         decode.GreedyDecoder(modeling.DecoderModel(cfg), fused=False)
+
+
+def test_bench_runs_one_gpu_only():
+    """bench.py measures one GPU: any other --gpus exits with status 2 and says why, before touching a device."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "8"], capture_output=True, text=True,
+                       timeout=120, cwd=root)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
