@@ -370,9 +370,9 @@ def beam_leg(pkg, torch, w: Workload, steps: int, warmup: int, reps: int) -> dic
     return res
 
 
-def time_prefill_real(pkg, torch, caches, width: int = 2048, reps: int = 3) -> dict:
+def time_prefill_real(pkg, torch, caches, width: int = 2048, reps: int = 10) -> dict:
     """The causal prefill at the real checkpoint's shape (8 contexts x ``width`` positions x 8 heads x 512, bf16):
-    verify attention over 16-position blocks, one launch pair per context (eager, HIP events)."""
+    one launch of the wide-head causal kernel (eager, HIP events)."""
     kernels = pkg.kernels
     heads, dim = caches.heads, caches.head_dim
     g = torch.Generator(device="cuda").manual_seed(1007)

@@ -1,7 +1,7 @@
 // Causal attention over whole contexts for gfx950: the prefill's
 //     F.scaled_dot_product_attention(q, k, v, is_causal=True)
 // (src/omniasr_trt/decode.py:163-164) over the cache rows ``kernels.rope_kv`` has just written.  Query p of context
-// b attends to keys [0, p] of its cache row; fp32 accumulation, bf16 in and out, head_dim 128.
+// b attends to keys [0, p] of its cache row; fp32 accumulation, bf16 in and out, head_dim 128, 256 or 512.
 #include <math.h>
 
 #include "attn_tiles.h"
@@ -28,14 +28,14 @@ constexpr int kPfChunks = kPfStage * 16 / kPfThreads;  // 16-byte chunks of K (a
 static_assert(kPfChunks * kPfThreads == kPfStage * 16, "a stage is whole chunks per thread");
 
 struct PrefillArgs {
-  const uint16_t* q;    // [B * width, H, 128] bf16
-  const uint16_t* k;    // cache rows: element strides s_row / s_head, key rows contiguous (128 elements)
+  const uint16_t* q;    // [B * width, H, D] bf16
+  const uint16_t* k;    // cache rows: element strides s_row / s_head, key rows contiguous (D elements)
   const uint16_t* v;
   const int64_t* slots;  // [B] cache row of each context
   int64_t s_row, s_head, cache_rows;
   int width, H;
   float scale_log2;
-  uint16_t* out;  // [B * width, H, 128] bf16
+  uint16_t* out;  // [B * width, H, D] bf16
 };
 
 // The softmax step of one 16-query group for one tile: mask (key0 + j >= lim), lazy reference max, this lane's
@@ -226,6 +226,168 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
   }
 }
 
+// Wide heads (D = 256, 512): one workgroup of kPwWaves waves per (query block, head, context), wave w holding the
+// 128-dimension slice sl = w % (D/128) of the queries of query wave m = w / (D/128) (kPwSub groups of 16).  Per
+// 32-key tile (K and V through LDS once for all waves): each wave writes its slice's partial scores S^T = K_sl Q_sl^T
+// to LDS; after a barrier every slice wave of query wave m adds the D/128 partials in the same order (so all of them
+// hold the same scores and probabilities), runs the lazy softmax and O_sl += P V_sl on its own slice of V.
+constexpr int kPwWaves = 8;
+constexpr int kPwSub = 2;  // 16-query groups per wave
+
+template <int D>
+__global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attn_wide_kernel(
+    PrefillArgs a) {
+  constexpr int NSL = D / 128, M = kPwWaves / NSL, QW = 16 * kPwSub * M;
+  constexpr int kRowB = D * 2 + 16;                        // LDS bytes per key row, padded against bank conflicts
+  constexpr int kRowChunks = D / 8;                        // 16-byte chunks per key row
+  constexpr int kChunks = 32 * kRowChunks / (64 * kPwWaves);  // chunks of K (and of V) per thread per tile
+  static_assert(NSL * M == kPwWaves && kChunks * 64 * kPwWaves == 32 * kRowChunks, "whole slices and chunks");
+  __shared__ __attribute__((aligned(16))) char kv[2][32 * kRowB];  // [K, V][32 key rows]
+  __shared__ f32x4_t part[M][kPwSub][NSL][2][64];                  // partial scores: [.., block mb][lane]
+  const int nqb = (a.width + QW - 1) / QW;
+  const int qb = (nqb - 1 - (int)blockIdx.x) * QW;  // the longest blocks first
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int sl = w % NSL, m = w / NSL;
+  const int64_t slot = clamp64(a.slots[b], 0, a.cache_rows - 1);
+  const uint16_t* kbase = a.k + slot * a.s_row + h * a.s_head;
+  const uint16_t* vbase = a.v + slot * a.s_row + h * a.s_head;
+  const int kend = min(qb + QW, a.width);
+  const int nt = (kend + 31) / 32;
+
+  // Global -> LDS: thread tid moves 16-byte chunks tid, tid + 64 kPwWaves, ... of the tile's K and V rows.  Rows past
+  // the context read its last key (finite: masked by the causal limit).
+  u32x4_t stage[2 * kChunks];
+  auto fetch = [&](int t) {
+#pragma unroll
+    for (int e = 0; e < kChunks; ++e) {
+      const int ci = tid + e * 64 * kPwWaves, r = ci / kRowChunks, col = ci % kRowChunks;
+      const int key = min(t * 32 + r, a.width - 1);
+      stage[e] = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)key * D + col * 8);
+      stage[kChunks + e] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)key * D + col * 8);
+    }
+  };
+  auto put = [&]() {
+#pragma unroll
+    for (int e = 0; e < kChunks; ++e) {
+      const int ci = tid + e * 64 * kPwWaves, r = ci / kRowChunks, col = ci % kRowChunks;
+      *reinterpret_cast<u32x4_t*>(&kv[0][r * kRowB + col * 16]) = stage[e];
+      *reinterpret_cast<u32x4_t*>(&kv[1][r * kRowB + col * 16]) = stage[kChunks + e];
+    }
+  };
+
+  int q0[kPwSub];
+  u32x4_t qop[kPwSub][4];  // lane (c, g): q[q0 + c][128 sl + 32 s2 + 8g .. +7] (0 past the end)
+  SoftmaxState st[kPwSub];
+  f32x4_t o[kPwSub][8];    // output column c of block e: dimension 128 sl + 16 e + c
+#pragma unroll
+  for (int u = 0; u < kPwSub; ++u) {
+    q0[u] = qb + 16 * (m + M * u);
+    const bool live = q0[u] + c < a.width;
+    const uint16_t* qrow = a.q + ((int64_t)(b * a.width + (live ? q0[u] + c : 0)) * a.H + h) * D + 128 * sl + g * 8;
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2)
+      qop[u][s2] = live ? *reinterpret_cast<const u32x4_t*>(qrow + s2 * 32) : u32x4_t{0u, 0u, 0u, 0u};
+    st[u] = SoftmaxState{-INFINITY, -INFINITY, 0.f};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[u][e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  fetch(0);
+  put();
+  lds_barrier();
+  for (int t = 0; t < nt; ++t) {
+    if (t + 1 < nt) fetch(t + 1);  // in flight during the tile's math
+    const int key0 = t * 32;
+    bool act[kPwSub];  // groups that see the tile: the same in every slice wave of query wave m
+#pragma unroll
+    for (int u = 0; u < kPwSub; ++u) act[u] = q0[u] < a.width && key0 <= q0[u] + 15;
+    {
+      u32x4_t kf[2][4];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const int rk = 8 * (c >> 2) + 4 * mb + (c & 3);
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+          kf[mb][s2] = *reinterpret_cast<const u32x4_t*>(&kv[0][rk * kRowB + 256 * sl + g * 16 + s2 * 64]);
+      }
+#pragma unroll
+      for (int u = 0; u < kPwSub; ++u) {
+        if (!act[u]) continue;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s2 = 0; s2 < 4; ++s2)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[mb][s2]),
+                                                          __builtin_bit_cast(bf16x8_t, qop[u][s2]), acc, 0, 0, 0);
+          part[m][u][sl][mb][lane] = acc;
+        }
+      }
+    }
+    lds_barrier();
+    u32x4_t pop[kPwSub];
+#pragma unroll
+    for (int u = 0; u < kPwSub; ++u) {
+      if (!act[u]) continue;
+      f32x4_t sum[2];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        sum[mb] = part[m][u][0][mb][lane];
+#pragma unroll
+        for (int s3 = 1; s3 < NSL; ++s3) sum[mb] += part[m][u][s3][mb][lane];
+      }
+      float sv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sv[j] = sum[j >> 2][j & 3];
+      pop[u] = softmax_tile<8>(sv, a.scale_log2, st[u], o[u], g, key0 + 8 * g, q0[u] + c + 1, key0 + 31 <= q0[u]);
+    }
+    {
+      // V operands by transpose reads, as in prefill_attn_kernel, from this wave's slice of the rows.
+      const int rr = c >> 2, q4 = c & 3;
+      const lds_char* vls = (const lds_char*)kv[1];  // kv lives in LDS
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int off = (8 * g + rr) * kRowB + 256 * sl + (16 * e + 4 * q4) * 2;
+        const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vls + off));
+        const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vls + off + 4 * kRowB));
+        u32x4_t bop;
+        bop[0] = (uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
+        bop[1] = (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
+        bop[2] = (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
+        bop[3] = (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
+#pragma unroll
+        for (int u = 0; u < kPwSub; ++u) {
+          if (!act[u]) continue;
+          o[u][e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pop[u]),
+                                                            __builtin_bit_cast(bf16x8_t, bop), o[u][e], 0, 0, 0);
+        }
+      }
+    }
+    lds_barrier();  // every wave is done with the tile's K, V and partial scores
+    if (t + 1 < nt) put();
+    lds_barrier();
+  }
+
+  // ---- each group's 16 output rows, this wave's slice: O / l, rounded to bf16
+#pragma unroll
+  for (int u = 0; u < kPwSub; ++u) {
+    float l_tot = st[u].l_run + __shfl_xor(st[u].l_run, 16, kWave);
+    l_tot += __shfl_xor(l_tot, 32, kWave);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float li = __shfl(l_tot, 4 * g + i, kWave);
+      const int qq = q0[u] + 4 * g + i;
+      if (qq >= a.width) continue;
+      const float div = li > 0.f ? li : 1.f;
+      uint16_t* orow = a.out + ((int64_t)(b * a.width + qq) * a.H + h) * D + 128 * sl;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) orow[16 * e + c] = (uint16_t)pack_bf16x2(o[u][e][i] / div, 0.f);
+    }
+  }
+}
+
 }  // namespace omni
 
 extern "C" int omni_prefill_attention(const void* q, const void* k_cache, const void* v_cache, int64_t stride_row,
@@ -235,13 +397,13 @@ extern "C" int omni_prefill_attention(const void* q, const void* k_cache, const 
                                       void* stream) {
   if (contexts < 0 || width < 0 || heads <= 0 || cache_rows <= 0) return OMNI_ERR_INVALID;
   if (dtype != OMNI_BF16) return OMNI_ERR_DTYPE;
-  if (head_dim != 128 || stride_pos != head_dim) return OMNI_ERR_SHAPE;
+  if ((head_dim != 128 && head_dim != 256 && head_dim != 512) || stride_pos != head_dim) return OMNI_ERR_SHAPE;
   if (!(scale > 0.f) || width > cache_len) return OMNI_ERR_INVALID;
   if (contexts == 0 || width == 0) return OMNI_OK;
   if (!q || !k_cache || !v_cache || !slots || !out) return OMNI_ERR_INVALID;
   if (((uintptr_t)q | (uintptr_t)out | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15u) return OMNI_ERR_INVALID;
   if ((stride_row | stride_head) % 8 != 0) return OMNI_ERR_INVALID;
-  if ((int64_t)contexts * width * heads >= (int64_t{1} << 31) / 128) return OMNI_ERR_INVALID;
+  if ((int64_t)contexts * width * heads >= (int64_t{1} << 31) / head_dim) return OMNI_ERR_INVALID;
   omni::PrefillArgs a;
   a.q = (const uint16_t*)q;
   a.k = (const uint16_t*)k_cache;
@@ -254,7 +416,17 @@ extern "C" int omni_prefill_attention(const void* q, const void* k_cache, const 
   a.H = heads;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.out = (uint16_t*)out;
-  dim3 grid((width + omni::kPfQueries - 1) / omni::kPfQueries, heads, contexts);
-  omni::prefill_attn_kernel<<<grid, 64 * omni::kPfWaves, 0, (hipStream_t)stream>>>(a);
+  hipStream_t s = (hipStream_t)stream;
+  if (head_dim == 128) {
+    dim3 grid((width + omni::kPfQueries - 1) / omni::kPfQueries, heads, contexts);
+    omni::prefill_attn_kernel<<<grid, 64 * omni::kPfWaves, 0, s>>>(a);
+  } else {
+    const int qw = 16 * omni::kPwSub * (omni::kPwWaves / (head_dim / 128));  // queries per workgroup
+    dim3 grid((width + qw - 1) / qw, heads, contexts);
+    if (head_dim == 256)
+      omni::prefill_attn_wide_kernel<256><<<grid, 64 * omni::kPwWaves, 0, s>>>(a);
+    else
+      omni::prefill_attn_wide_kernel<512><<<grid, 64 * omni::kPwWaves, 0, s>>>(a);
+  }
   return omni_launch_status();
 }

@@ -19,9 +19,8 @@ the verify logits and the acceptance); for the prefill: :func:`prefill_attention
 contexts, the reference's ``F.scaled_dot_product_attention(is_causal=True)``).
 
 Nothing here synchronises or allocates beyond the outputs and the attention workspace (from torch's
-allocator, so from a graph's pool under capture), so every function can be captured in a HIP graph -- except
-:func:`prefill_attention` at head dims 256 / 512, which reads the contexts' cache rows on the host (the decoders
-run the prefill eagerly).  There is no other code path: on a GPU without the library these functions raise.
+allocator, so from a graph's pool under capture), so every function can be captured in a HIP graph.  There is
+no other code path: on a GPU without the library these functions raise.
 """
 
 from __future__ import annotations
@@ -218,8 +217,8 @@ def beam_attention(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, ctx_len:
 
 def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, slots: torch.Tensor,
                       width: int, scale: float) -> torch.Tensor:
-    """Causal attention of whole contexts over their cache rows: ``q`` [B*width, H, D] bf16, D = 128 (the causal kernel)
-    or 256 / 512 (see :func:`_prefill_by_blocks`) (context b's queries at rows b*width ..), ``k_cache``/``v_cache``
+    """Causal attention of whole contexts over their cache rows: ``q`` [B*width, H, D] bf16, D = 128, 256 or 512
+    (context b's queries at rows b*width ..), ``k_cache``/``v_cache``
     [rows, H, S >= width, D] bf16 with unit stride in D, ``slots`` [B]
     the contexts' cache rows; query p of context b attends to keys [0, p] of row ``slots[b]``.  Returns
     [B*width, H, D] -- ``F.scaled_dot_product_attention(q, k, v, is_causal=True)`` of the prefill
@@ -236,8 +235,6 @@ def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
     _need(k_cache.size(2) >= width, "caches: at least width positions")
     _index(slots, "slots")
     _need(slots.numel() >= contexts, "slots: [B]")
-    if dim in (256, 512) and q.dtype == torch.bfloat16:
-        return _prefill_by_blocks(q, k_cache, v_cache, slots, width, scale)
     out = torch.empty_like(q)
     status = lib.omni_prefill_attention(
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
@@ -247,34 +244,8 @@ def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
     return out
 
 
-def _prefill_by_blocks(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, slots: torch.Tensor,
-                       width: int, scale: float) -> torch.Tensor:
-    """Head dims 256 / 512: the causal prefill as verify attention over blocks of 32 positions.  Block j of a context
-    is a verify row whose 32 queries are positions 32j .. 32j + 31 with ``lengths = 32j + 1``, so query i sees keys
-    [0, 32j + i] -- the causal mask; every block of a context reads the context's cache row (row stride 0).  One
-    launch per context (the cache rows are read on the host); positions past the width are computed on zero
-    queries and dropped."""
-    rows, heads, dim = q.shape
-    contexts = rows // width
-    blk = 32  # positions per block: two 16-query groups per wave
-    blocks = -(-width // blk)
-    padded = blocks * blk
-    lengths = torch.arange(0, padded, blk, device=q.device, dtype=torch.long) + 1
-    keys = min(-(-padded // 256) * 256, k_cache.size(2))
-    out = torch.empty_like(q)
-    qb = torch.zeros(padded, heads, dim, device=q.device, dtype=q.dtype)
-    for b, row in enumerate(slots[:contexts].tolist()):
-        qb[:width] = q[b * width:(b + 1) * width]
-        kc = k_cache[row].unsqueeze(0).expand(blocks, -1, -1, -1)
-        vc = v_cache[row].unsqueeze(0).expand(blocks, -1, -1, -1)
-        o = _verify(qb, kc, vc, lengths, blk, keys, scale, 0, True)
-        out[b * width:(b + 1) * width] = o[:width]
-    return out
-
-
 def prefill_supported(dtype: torch.dtype, head_dim: int) -> bool:
-    """Whether :func:`prefill_attention` covers this element type and head size: bf16 with head dim 128 (the causal
-    kernel) or 256 / 512 (verify attention over 32-position blocks)."""
+    """Whether :func:`prefill_attention` covers this element type and head size: bf16 with head dim 128, 256 or 512."""
     return dtype == torch.bfloat16 and head_dim in (128, 256, 512)
 
 

@@ -157,7 +157,7 @@ def test_graph_replays_equal_eager_steps(cuda):
 
 @pytest.mark.parametrize("model_dim,heads", [(256, 2), (512, 1)])
 def test_bf16_prefill_kernel_matches_torch_attention(cuda, monkeypatch, model_dim, heads):
-    """A bf16 model with head dim 128 (the causal kernel) or 512 (32-position verify blocks): the prefill through
+    """A bf16 model with head dim 128 (the causal kernel) or 512 (the slice-per-wave kernel): the prefill through
     kernels.prefill_attention gives the log-probabilities of the fp32 torch attention path within bf16 tolerance,
     for contexts of different lengths in permuted cache rows."""
     torch.manual_seed(31)
