@@ -38,6 +38,22 @@ struct PrefillArgs {
   uint16_t* out;  // [B * width, H, D] bf16
 };
 
+// Workgroup -> (query block j counted from the longest, head h, context b).  The dispatcher hands consecutive
+// workgroups to the 8 XCDs in turn; when heads x contexts is a multiple of 8, XCD x gets units (head, context)
+// x, x + 8, ... one after another, all query blocks of a unit together (longest first), so each unit's K / V rows
+// are brought into one XCD's L2 rather than into all eight.  Only speed depends on the dispatch order.
+constexpr bool kPfXcd = true;
+struct PfBlock {
+  int j, h, b;
+};
+__device__ __forceinline__ PfBlock pf_block(int nqb, int H, int B) {
+  if (!kPfXcd || (H * B) % 8 != 0) return PfBlock{(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
+  const int L = (int)blockIdx.x + nqb * ((int)blockIdx.y + H * (int)blockIdx.z);
+  const int x = L % 8, k = L / 8;
+  const int unit = (k / nqb) * 8 + x;
+  return PfBlock{k % nqb, unit % H, unit / H};
+}
+
 // The softmax step of one 16-query group for one tile: mask (key0 + j >= lim), lazy reference max, this lane's
 // 8 probabilities packed as the P operand.  (The same arithmetic as attend().)
 template <int NB>
@@ -80,8 +96,9 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
   constexpr int D = 128, KS = D / 32;
   __shared__ __attribute__((aligned(16))) char lds[2][2][kPfStage * kPfRow];  // [buffer][K, V][key rows]
   const int nqb = (a.width + kPfQueries - 1) / kPfQueries;
-  const int qb = (nqb - 1 - (int)blockIdx.x) * kPfQueries;  // the longest blocks first
-  const int h = blockIdx.y, b = blockIdx.z;
+  const PfBlock blk = pf_block(nqb, a.H, (int)gridDim.z);
+  const int qb = (nqb - 1 - blk.j) * kPfQueries;  // the longest blocks first
+  const int h = blk.h, b = blk.b;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t slot = clamp64(a.slots[b], 0, a.cache_rows - 1);
@@ -232,7 +249,7 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
 // to LDS; after a barrier every slice wave of query wave m adds the D/128 partials in the same order (so all of them
 // hold the same scores and probabilities), runs the lazy softmax and O_sl += P V_sl on its own slice of V.
 constexpr int kPwWaves = 8;
-constexpr int kPwSub = 2;  // 16-query groups per wave
+constexpr int kPwSub = 3;  // 16-query groups per wave (3: 8 VGPRs spilled at D = 512, still the fastest of 2 and 3)
 
 template <int D>
 __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attn_wide_kernel(
@@ -245,8 +262,9 @@ __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2
   __shared__ __attribute__((aligned(16))) char kv[2][32 * kRowB];  // [K, V][32 key rows]
   __shared__ f32x4_t part[M][kPwSub][NSL][2][64];                  // partial scores: [.., block mb][lane]
   const int nqb = (a.width + QW - 1) / QW;
-  const int qb = (nqb - 1 - (int)blockIdx.x) * QW;  // the longest blocks first
-  const int h = blockIdx.y, b = blockIdx.z;
+  const PfBlock blk = pf_block(nqb, a.H, (int)gridDim.z);
+  const int qb = (nqb - 1 - blk.j) * QW;  // the longest blocks first
+  const int h = blk.h, b = blk.b;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int sl = w % NSL, m = w / NSL;

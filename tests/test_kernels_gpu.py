@@ -133,11 +133,11 @@ def test_verify_attention_wide_heads_up_to_32_queries(cuda, t, d):
 
 
 @pytest.mark.parametrize("width,d", [(1, 128), (15, 128), (64, 128), (97, 128), (300, 128), (1, 512), (15, 512),
-                                     (64, 512), (97, 512), (300, 512), (1, 256), (128, 256), (300, 256)])
+                                     (96, 512), (97, 512), (300, 512), (1, 256), (192, 256), (300, 256)])
 def test_prefill_attention(cuda, width, d):
     """Causal attention over whole contexts (src/omniasr_trt/decode.py:163-164) against the oracle's verify attention
     with query p of a context over keys [0, p]: cache rows addressed through slots, widths that are not multiples
-    of the query block (192 queries at head dim 128, 128 at 256, 64 at 512) or of the 32-key tile."""
+    of the query block (192 queries at head dims 128 and 256, 96 at 512) or of the 32-key tile."""
     g = gen(60 + width)
     b, h, rows, cap = 3, 4, 5, 320
     kc = torch.randn(rows, h, cap, d, generator=g).to(torch.bfloat16)
