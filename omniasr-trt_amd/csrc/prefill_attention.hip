@@ -286,12 +286,11 @@ __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2
       stage[kChunks + e] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)key * D + col * 8);
     }
   };
-  auto put = [&]() {
+  auto put = [&](int which) {  // 0: K, 1: V
 #pragma unroll
     for (int e = 0; e < kChunks; ++e) {
       const int ci = tid + e * 64 * kPwWaves, r = ci / kRowChunks, col = ci % kRowChunks;
-      *reinterpret_cast<u32x4_t*>(&kv[0][r * kRowB + col * 16]) = stage[e];
-      *reinterpret_cast<u32x4_t*>(&kv[1][r * kRowB + col * 16]) = stage[kChunks + e];
+      *reinterpret_cast<u32x4_t*>(&kv[which][r * kRowB + col * 16]) = stage[which * kChunks + e];
     }
   };
 
@@ -312,8 +311,12 @@ __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2
     for (int e = 0; e < 8; ++e) o[u][e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
+  // Two barriers per tile: after the first, every wave has read the tile's K (its partial scores are written), so
+  // the next tile's K goes in; after the second, every wave has read the tile's V and the partial scores, so the
+  // next tile's V goes in (the next tile's first barrier publishes it before its P V).
   fetch(0);
-  put();
+  put(0);
+  put(1);
   lds_barrier();
   for (int t = 0; t < nt; ++t) {
     if (t + 1 < nt) fetch(t + 1);  // in flight during the tile's math
@@ -345,6 +348,7 @@ __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2
       }
     }
     lds_barrier();
+    if (t + 1 < nt) put(0);
     u32x4_t pop[kPwSub];
 #pragma unroll
     for (int u = 0; u < kPwSub; ++u) {
@@ -383,9 +387,8 @@ __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2
         }
       }
     }
-    lds_barrier();  // every wave is done with the tile's K, V and partial scores
-    if (t + 1 < nt) put();
-    lds_barrier();
+    lds_barrier();  // every wave is done with the tile's V and partial scores; the next tile's K is in
+    if (t + 1 < nt) put(1);
   }
 
   // ---- each group's 16 output rows, this wave's slice: O / l, rounded to bf16
