@@ -276,21 +276,21 @@ __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2
 
   // Global -> LDS: thread tid moves 16-byte chunks tid, tid + 64 kPwWaves, ... of the tile's K and V rows.  Rows past
   // the context read its last key (finite: masked by the causal limit).
-  u32x4_t stage[2 * kChunks];
-  auto fetch = [&](int t) {
+  u32x4_t stage[kChunks];  // one of K, V at a time
+  auto fetch = [&](int t, int which) {  // 0: K, 1: V
+    const uint16_t* base = which ? vbase : kbase;
 #pragma unroll
     for (int e = 0; e < kChunks; ++e) {
       const int ci = tid + e * 64 * kPwWaves, r = ci / kRowChunks, col = ci % kRowChunks;
       const int key = min(t * 32 + r, a.width - 1);
-      stage[e] = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)key * D + col * 8);
-      stage[kChunks + e] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)key * D + col * 8);
+      stage[e] = *reinterpret_cast<const u32x4_t*>(base + (int64_t)key * D + col * 8);
     }
   };
-  auto put = [&](int which) {  // 0: K, 1: V
+  auto put = [&](int which) {
 #pragma unroll
     for (int e = 0; e < kChunks; ++e) {
       const int ci = tid + e * 64 * kPwWaves, r = ci / kRowChunks, col = ci % kRowChunks;
-      *reinterpret_cast<u32x4_t*>(&kv[which][r * kRowB + col * 16]) = stage[which * kChunks + e];
+      *reinterpret_cast<u32x4_t*>(&kv[which][r * kRowB + col * 16]) = stage[e];
     }
   };
 
@@ -312,14 +312,15 @@ __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2
   }
 
   // Two barriers per tile: after the first, every wave has read the tile's K (its partial scores are written), so
-  // the next tile's K goes in; after the second, every wave has read the tile's V and the partial scores, so the
-  // next tile's V goes in (the next tile's first barrier publishes it before its P V).
-  fetch(0);
+  // the next tile's K goes in and its V is fetched; after the second, every wave has read the tile's V and the
+  // partial scores, so the next tile's V goes in (the next tile's first barrier publishes it before its P V).
+  fetch(0, 0);
   put(0);
+  fetch(0, 1);
   put(1);
   lds_barrier();
   for (int t = 0; t < nt; ++t) {
-    if (t + 1 < nt) fetch(t + 1);  // in flight during the tile's math
+    if (t + 1 < nt) fetch(t + 1, 0);  // the next K, in flight during the partial scores
     const int key0 = t * 32;
     bool act[kPwSub];  // groups that see the tile: the same in every slice wave of query wave m
 #pragma unroll
@@ -348,7 +349,10 @@ __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2
       }
     }
     lds_barrier();
-    if (t + 1 < nt) put(0);
+    if (t + 1 < nt) {
+      put(0);
+      fetch(t + 1, 1);  // the next V, in flight during the softmax and P V
+    }
     u32x4_t pop[kPwSub];
 #pragma unroll
     for (int u = 0; u < kPwSub; ++u) {
