@@ -372,14 +372,15 @@ def beam_leg(pkg, torch, w: Workload, steps: int, warmup: int, reps: int) -> dic
 
 def time_prefill_real(pkg, torch, caches, width: int = 2048, reps: int = 10) -> dict:
     """The causal prefill at the real checkpoint's shape (8 contexts x ``width`` positions x 8 heads x 512, bf16):
-    one launch of the wide-head causal kernel (eager, HIP events)."""
+    one launch of the wide-head causal kernel per call, three untimed calls first (eager, HIP events)."""
     kernels = pkg.kernels
     heads, dim = caches.heads, caches.head_dim
     g = torch.Generator(device="cuda").manual_seed(1007)
     q = torch.randn(SLOTS * width, heads, dim, device="cuda", generator=g).to(torch.bfloat16)
     rows = torch.arange(SLOTS, device="cuda")
     call = lambda: kernels.prefill_attention(q, caches.k[0], caches.v[0], rows, width, dim ** -0.5)
-    call()
+    for _ in range(3):
+        call()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()

@@ -132,19 +132,22 @@ def test_verify_attention_wide_heads_up_to_32_queries(cuda, t, d):
         kernels.draft_attention(q, kc, kc, torch.tensor([5, 9], device=cuda), 17, 256, 0.1)
 
 
-@pytest.mark.parametrize("width,d", [(1, 128), (15, 128), (64, 128), (97, 128), (300, 128), (1, 512), (15, 512),
-                                     (96, 512), (97, 512), (300, 512), (1, 256), (192, 256), (300, 256)])
-def test_prefill_attention(cuda, width, d):
+@pytest.mark.parametrize("width,d,b,h", [(1, 128, 3, 4), (15, 128, 3, 4), (64, 128, 3, 4), (97, 128, 3, 4),
+                                         (300, 128, 3, 4), (1, 512, 3, 4), (15, 512, 3, 4), (96, 512, 3, 4),
+                                         (97, 512, 3, 4), (300, 512, 3, 4), (1, 256, 3, 4), (192, 256, 3, 4),
+                                         (300, 256, 3, 4), (300, 128, 4, 2), (400, 512, 2, 4), (250, 256, 8, 1)])
+def test_prefill_attention(cuda, width, d, b, h):
     """Causal attention over whole contexts (src/omniasr_trt/decode.py:163-164) against the oracle's verify attention
     with query p of a context over keys [0, p]: cache rows addressed through slots, widths that are not multiples
-    of the query block (192 queries at head dims 128 and 256, 96 at 512) or of the 32-key tile."""
+    of the query block (192 queries at head dims 128 and 256, 96 at 512) or of the 32-key tile; heads x contexts a
+    multiple of 8 (the XCD-ordered workgroup map) or not (the plain one)."""
     g = gen(60 + width)
-    b, h, rows, cap = 3, 4, 5, 320
+    rows, cap = 5, 448
     kc = torch.randn(rows, h, cap, d, generator=g).to(torch.bfloat16)
     vc = torch.randn(rows, h, cap, d, generator=g).to(torch.bfloat16)
     q = torch.randn(b * width, h, d, generator=g).to(torch.bfloat16)
-    slots = torch.tensor([4, 0, 2])
-    say(f"prefill attention width={width} d={d}")
+    slots = torch.tensor([4, 0, 2, 1, 3, 0, 4, 2])[:b]
+    say(f"prefill attention width={width} d={d} contexts={b} heads={h}")
     out = kernels.prefill_attention(q.to(cuda), kc.to(cuda), vc.to(cuda), slots.to(cuda), width, d ** -0.5)
     torch.cuda.synchronize()
     sl = slots.numpy()
