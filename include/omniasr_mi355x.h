@@ -155,7 +155,8 @@ int omni_beam_attention(const void *q, const void *k_ctx, const void *v_ctx, int
  * K / V caches: element strides stride_row / stride_head / stride_pos, cache_len >= width positions.
  * bf16, head_dim 128, 256 or 512, contiguous key rows (stride_pos == head_dim); fp32 accumulation.  No workspace.
  * Head dim 128: one workgroup of 4 waves x 48 queries per 192-query block; 256 / 512: one workgroup of 8 waves per
- * 192 / 96-query block, each wave one 128-dimension slice, partial scores added through LDS.
+ * 192 / 96-query block, each wave one 128-dimension slice, partial scores added through LDS and each 16-query
+ * group's softmax run by one wave.
  */
 int omni_prefill_attention(const void *q, const void *k_cache, const void *v_cache, int64_t stride_row,
                            int64_t stride_head, int64_t stride_pos, int64_t cache_len, int64_t cache_rows,

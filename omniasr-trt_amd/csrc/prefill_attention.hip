@@ -243,24 +243,37 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
   }
 }
 
-// Wide heads (D = 256, 512): one workgroup of kPwWaves waves per (query block, head, context), wave w holding the
-// 128-dimension slice sl = w % (D/128) of the queries of query wave m = w / (D/128) (kPwSub groups of 16).  Per
-// 32-key tile (K and V through LDS once for all waves): each wave writes its slice's partial scores S^T = K_sl Q_sl^T
-// to LDS; after a barrier every slice wave of query wave m adds the D/128 partials in the same order (so all of them
-// hold the same scores and probabilities), runs the lazy softmax and O_sl += P V_sl on its own slice of V.
+// Wide heads (D = 256, 512): one workgroup of kPwWaves waves per (query block, head, context).  The block's
+// NG = kPwSub * M groups of 16 queries (M = kPwWaves / (D/128)): group gi holds queries qb + 16 gi .. + 15.  Wave w
+// holds the 128-dimension slice sl = w % (D/128) of q and O for the groups m + M u (m = w / (D/128), u < kPwSub).
+// Per 32-key tile (K and V through LDS once for all waves):
+//   1. each wave writes its slice's partial scores S^T = K_sl Q_sl^T of its groups to LDS;  barrier;
+//   2. wave w runs the softmax of groups w, w + kPwWaves, ...: adds the D/128 partials in slice order, moves the
+//      lazy reference max when needed, and publishes the group's P operand (bf16) and, when the reference max
+//      moved, its 16 rescale factors;  barrier;
+//   3. each wave rescales its O_sl of a group when told to and adds P V_sl.
+// So each group's softmax runs once, not once per slice.  K has one LDS buffer (the next tile's goes in after
+// barrier 1, when every wave has read this one), V two (the next tile's goes in during step 3 of this one, into the
+// buffer the previous tile's P V read before barrier 1).
 constexpr int kPwWaves = 8;
-constexpr int kPwSub = 3;  // 16-query groups per wave (3: 8 VGPRs spilled at D = 512, still the fastest of 2 and 3)
+constexpr int kPwSub = 3;  // 16-query groups per wave
 
 template <int D>
 __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attn_wide_kernel(
     PrefillArgs a) {
-  constexpr int NSL = D / 128, M = kPwWaves / NSL, QW = 16 * kPwSub * M;
-  constexpr int kRowB = D * 2 + 16;                        // LDS bytes per key row, padded against bank conflicts
-  constexpr int kRowChunks = D / 8;                        // 16-byte chunks per key row
-  constexpr int kChunks = 32 * kRowChunks / (64 * kPwWaves);  // chunks of K (and of V) per thread per tile
+  constexpr int NSL = D / 128, M = kPwWaves / NSL, NG = kPwSub * M, QW = 16 * NG;
+  constexpr int OWN = (NG + kPwWaves - 1) / kPwWaves;  // groups whose softmax one wave runs, at most
+  constexpr int kRowB = D * 2 + 16;                     // LDS bytes per key row, padded against bank conflicts
+  constexpr int kRowChunks = D / 8;                     // 16-byte chunks per key row
+  constexpr int kChunks = 32 * kRowChunks / (64 * kPwWaves);  // chunks of K (or of V) per thread per tile
   static_assert(NSL * M == kPwWaves && kChunks * 64 * kPwWaves == 32 * kRowChunks, "whole slices and chunks");
-  __shared__ __attribute__((aligned(16))) char kv[2][32 * kRowB];  // [K, V][32 key rows]
-  __shared__ f32x4_t part[M][kPwSub][NSL][2][64];                  // partial scores: [.., block mb][lane]
+  __shared__ __attribute__((aligned(16))) char kl[32 * kRowB];     // K: 32 key rows
+  __shared__ __attribute__((aligned(16))) char vl[2][32 * kRowB];  // V: two tiles
+  __shared__ f32x4_t part[NG][NSL][2][64];  // partial scores: [group][slice][block mb][lane]
+  __shared__ u32x4_t pex[NG][64];           // P operand of each group: [group][lane]
+  __shared__ float alx[NG][16];             // rescale factor of each query of a group (when rflag)
+  __shared__ int rflag[NG];                 // the group's reference max moved on this tile
+  __shared__ float lsum[NG][16];            // probability sum of each query, at the end
   const int nqb = (a.width + QW - 1) / QW;
   const PfBlock blk = pf_block(nqb, a.H, (int)gridDim.z);
   const int qb = (nqb - 1 - blk.j) * QW;  // the longest blocks first
@@ -274,11 +287,10 @@ __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2
   const int kend = min(qb + QW, a.width);
   const int nt = (kend + 31) / 32;
 
-  // Global -> LDS: thread tid moves 16-byte chunks tid, tid + 64 kPwWaves, ... of the tile's K and V rows.  Rows past
-  // the context read its last key (finite: masked by the causal limit).
-  u32x4_t stage[kChunks];  // one of K, V at a time
-  auto fetch = [&](int t, int which) {  // 0: K, 1: V
-    const uint16_t* base = which ? vbase : kbase;
+  // Global -> LDS through one set of staging registers: thread tid moves 16-byte chunks tid, tid + 64 kPwWaves, ...
+  // of a tile's K or V rows.  Rows past the context read its last key (finite: masked by the causal limit).
+  u32x4_t stage[kChunks];
+  auto fetch = [&](int t, const uint16_t* base) {
 #pragma unroll
     for (int e = 0; e < kChunks; ++e) {
       const int ci = tid + e * 64 * kPwWaves, r = ci / kRowChunks, col = ci % kRowChunks;
@@ -286,45 +298,42 @@ __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2
       stage[e] = *reinterpret_cast<const u32x4_t*>(base + (int64_t)key * D + col * 8);
     }
   };
-  auto put = [&](int which) {
+  auto put = [&](char* dst) {
 #pragma unroll
     for (int e = 0; e < kChunks; ++e) {
       const int ci = tid + e * 64 * kPwWaves, r = ci / kRowChunks, col = ci % kRowChunks;
-      *reinterpret_cast<u32x4_t*>(&kv[which][r * kRowB + col * 16]) = stage[e];
+      *reinterpret_cast<u32x4_t*>(dst + r * kRowB + col * 16) = stage[e];
     }
   };
+  // Whether group gi sees the tile starting at key0: a live group whose last query reaches the tile's first key.
+  auto sees = [&](int gi, int key0) { return qb + 16 * gi < a.width && key0 <= qb + 16 * gi + 15; };
 
-  int q0[kPwSub];
-  u32x4_t qop[kPwSub][4];  // lane (c, g): q[q0 + c][128 sl + 32 s2 + 8g .. +7] (0 past the end)
-  SoftmaxState st[kPwSub];
+  u32x4_t qop[kPwSub][4];  // lane (c, g): q[qb + 16 gi + c][128 sl + 32 s2 + 8g .. +7] (0 past the end)
   f32x4_t o[kPwSub][8];    // output column c of block e: dimension 128 sl + 16 e + c
 #pragma unroll
   for (int u = 0; u < kPwSub; ++u) {
-    q0[u] = qb + 16 * (m + M * u);
-    const bool live = q0[u] + c < a.width;
-    const uint16_t* qrow = a.q + ((int64_t)(b * a.width + (live ? q0[u] + c : 0)) * a.H + h) * D + 128 * sl + g * 8;
+    const int row = qb + 16 * (m + M * u) + c;
+    const bool live = row < a.width;
+    const uint16_t* qrow = a.q + ((int64_t)(b * a.width + (live ? row : 0)) * a.H + h) * D + 128 * sl + g * 8;
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2)
       qop[u][s2] = live ? *reinterpret_cast<const u32x4_t*>(qrow + s2 * 32) : u32x4_t{0u, 0u, 0u, 0u};
-    st[u] = SoftmaxState{-INFINITY, -INFINITY, 0.f};
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[u][e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
+  SoftmaxState st[OWN];  // the softmax state of groups w + kPwWaves r
+#pragma unroll
+  for (int r = 0; r < OWN; ++r) st[r] = SoftmaxState{-INFINITY, -INFINITY, 0.f};
 
-  // Two barriers per tile: after the first, every wave has read the tile's K (its partial scores are written), so
-  // the next tile's K goes in and its V is fetched; after the second, every wave has read the tile's V and the
-  // partial scores, so the next tile's V goes in (the next tile's first barrier publishes it before its P V).
-  fetch(0, 0);
-  put(0);
-  fetch(0, 1);
-  put(1);
+  fetch(0, kbase);
+  put(kl);
+  fetch(0, vbase);
+  put(vl[0]);
+  if (nt > 1) fetch(1, kbase);
   lds_barrier();
   for (int t = 0; t < nt; ++t) {
-    if (t + 1 < nt) fetch(t + 1, 0);  // the next K, in flight during the partial scores
     const int key0 = t * 32;
-    bool act[kPwSub];  // groups that see the tile: the same in every slice wave of query wave m
-#pragma unroll
-    for (int u = 0; u < kPwSub; ++u) act[u] = q0[u] < a.width && key0 <= q0[u] + 15;
+    // 1. partial scores of this wave's groups over its slice
     {
       u32x4_t kf[2][4];
 #pragma unroll
@@ -332,11 +341,12 @@ __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2
         const int rk = 8 * (c >> 2) + 4 * mb + (c & 3);
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2)
-          kf[mb][s2] = *reinterpret_cast<const u32x4_t*>(&kv[0][rk * kRowB + 256 * sl + g * 16 + s2 * 64]);
+          kf[mb][s2] = *reinterpret_cast<const u32x4_t*>(&kl[rk * kRowB + 256 * sl + g * 16 + s2 * 64]);
       }
 #pragma unroll
       for (int u = 0; u < kPwSub; ++u) {
-        if (!act[u]) continue;
+        const int gi = m + M * u;
+        if (!sees(gi, key0)) continue;
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
           f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -344,35 +354,88 @@ __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2
           for (int s2 = 0; s2 < 4; ++s2)
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[mb][s2]),
                                                           __builtin_bit_cast(bf16x8_t, qop[u][s2]), acc, 0, 0, 0);
-          part[m][u][sl][mb][lane] = acc;
+          part[gi][sl][mb][lane] = acc;
         }
       }
     }
     lds_barrier();
     if (t + 1 < nt) {
-      put(0);
-      fetch(t + 1, 1);  // the next V, in flight during the softmax and P V
+      put(kl);             // every wave has read this tile's K
+      fetch(t + 1, vbase);  // the next V, in flight during steps 2 and 3
     }
-    u32x4_t pop[kPwSub];
+    // 2. the softmax of this wave's own groups
 #pragma unroll
-    for (int u = 0; u < kPwSub; ++u) {
-      if (!act[u]) continue;
+    for (int r = 0; r < OWN; ++r) {
+      const int gi = w + kPwWaves * r;
+      if (gi >= NG || !sees(gi, key0)) continue;
+      const int q0 = qb + 16 * gi;
       f32x4_t sum[2];
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
-        sum[mb] = part[m][u][0][mb][lane];
+        sum[mb] = part[gi][0][mb][lane];
 #pragma unroll
-        for (int s3 = 1; s3 < NSL; ++s3) sum[mb] += part[m][u][s3][mb][lane];
+        for (int s3 = 1; s3 < NSL; ++s3) sum[mb] += part[gi][s3][mb][lane];
       }
       float sv[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) sv[j] = sum[j >> 2][j & 3];
-      pop[u] = softmax_tile<8>(sv, a.scale_log2, st[u], o[u], g, key0 + 8 * g, q0[u] + c + 1, key0 + 31 <= q0[u]);
+      const int lim = q0 + c + 1;
+      if (!(key0 + 31 <= q0)) {  // not every query of the group sees the whole tile
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sv[j] = key0 + 8 * g + j < lim ? sv[j] : -INFINITY;
+      }
+      bool over = false;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) over |= sv[j] > st[r].thr;
+      const bool moved = __any(over);
+      if (moved) {
+        float mx = sv[0];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sv[j]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const float m_new = fmaxf(st[r].m_ref, mx * a.scale_log2);
+        const float alpha = __builtin_amdgcn_exp2f(st[r].m_ref - (m_new == -INFINITY ? 0.f : m_new));  // -inf: 0
+        st[r].l_run *= alpha;
+        if (g == 0) alx[gi][c] = alpha;
+        st[r].m_ref = m_new;
+        st[r].thr = m_new == -INFINITY ? -INFINITY : (m_new + kLazyLog2) / a.scale_log2;
+      }
+      if (lane == 0) rflag[gi] = moved ? 1 : 0;
+      const float m_use = st[r].m_ref == -INFINITY ? 0.f : st[r].m_ref;
+      float p[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], a.scale_log2, -m_use));
+        st[r].l_run += p[j];
+      }
+      u32x4_t pop;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        pop[q] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{p[2 * q], p[2 * q + 1]}), bf16x2_t));
+      pex[gi][lane] = pop;
     }
+    lds_barrier();
+    // 3. O_sl += P V_sl for this wave's groups (rescaled first when the group's reference max moved)
     {
+      u32x4_t pop[kPwSub];
+#pragma unroll
+      for (int u = 0; u < kPwSub; ++u) {
+        const int gi = m + M * u;
+        if (!sees(gi, key0)) continue;
+        if (rflag[gi]) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float al = alx[gi][4 * g + i];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[u][e][i] *= al;
+          }
+        }
+        pop[u] = pex[gi][lane];
+      }
       // V operands by transpose reads, as in prefill_attn_kernel, from this wave's slice of the rows.
       const int rr = c >> 2, q4 = c & 3;
-      const lds_char* vls = (const lds_char*)kv[1];  // kv lives in LDS
+      const lds_char* vls = (const lds_char*)vl[t & 1];  // vl lives in LDS
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int off = (8 * g + rr) * kRowB + 256 * sl + (16 * e + 4 * q4) * 2;
@@ -385,26 +448,36 @@ __global__ __launch_bounds__(64 * kPwWaves) __attribute__((amdgpu_waves_per_eu(2
         bop[3] = (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
 #pragma unroll
         for (int u = 0; u < kPwSub; ++u) {
-          if (!act[u]) continue;
+          if (!sees(m + M * u, key0)) continue;
           o[u][e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pop[u]),
                                                             __builtin_bit_cast(bf16x8_t, bop), o[u][e], 0, 0, 0);
         }
       }
     }
-    lds_barrier();  // every wave is done with the tile's V and partial scores; the next tile's K is in
-    if (t + 1 < nt) put(1);
+    if (t + 1 < nt) {
+      put(vl[(t + 1) & 1]);  // read last by tile t - 1's P V, before this tile's first barrier
+      if (t + 2 < nt) fetch(t + 2, kbase);
+    }
   }
 
-  // ---- each group's 16 output rows, this wave's slice: O / l, rounded to bf16
+  // ---- probability sums from the softmax owners, then each group's 16 output rows of this wave's slice
+#pragma unroll
+  for (int r = 0; r < OWN; ++r) {
+    const int gi = w + kPwWaves * r;
+    if (gi >= NG) continue;
+    float l_tot = st[r].l_run + __shfl_xor(st[r].l_run, 16, kWave);
+    l_tot += __shfl_xor(l_tot, 32, kWave);
+    if (g == 0) lsum[gi][c] = l_tot;
+  }
+  lds_barrier();
 #pragma unroll
   for (int u = 0; u < kPwSub; ++u) {
-    float l_tot = st[u].l_run + __shfl_xor(st[u].l_run, 16, kWave);
-    l_tot += __shfl_xor(l_tot, 32, kWave);
+    const int gi = m + M * u;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float li = __shfl(l_tot, 4 * g + i, kWave);
-      const int qq = q0[u] + 4 * g + i;
+      const int qq = qb + 16 * gi + 4 * g + i;
       if (qq >= a.width) continue;
+      const float li = lsum[gi][4 * g + i];
       const float div = li > 0.f ? li : 1.f;
       uint16_t* orow = a.out + ((int64_t)(b * a.width + qq) * a.H + h) * D + 128 * sl;
 #pragma unroll
