@@ -1444,6 +1444,9 @@ __global__ __launch_bounds__(64) void beam_gen_kernel_d128(BeamGenArgs a) {
   constexpr int D = 128, kRow = D / 8;  // 16 lanes read a row
   const int h = blockIdx.x, r = blockIdx.y;
   const int lane = threadIdx.x, grp = lane / kRow, sub = lane - grp * kRow;
+  // The first 64 keys' row pointers load beside the length (the index is clamped into the row's capacity, so the
+  // load is in bounds whatever the length): one memory round trip less before the K / V loads.
+  const int32_t ptr0 = a.ptr[(int64_t)r * a.ptr_stride + (lane < a.gen_cap ? lane : a.gen_cap - 1)];
   const int64_t n = clamp64(a.gen_len[r], 0, a.gen_cap);
   float qv[8];
   {
@@ -1460,7 +1463,7 @@ __global__ __launch_bounds__(64) void beam_gen_kernel_d128(BeamGenArgs a) {
   for (int64_t j0 = 0; j0 < n; j0 += kWave) {
     const int64_t j = j0 + lane;
     const bool valid = j < n;
-    int64_t src = valid ? (int64_t)a.ptr[(int64_t)r * a.ptr_stride + j] : 0;
+    int64_t src = valid ? (j0 == 0 ? (int64_t)ptr0 : (int64_t)a.ptr[(int64_t)r * a.ptr_stride + j]) : 0;
     src = clamp64(src, 0, a.gen_rows - 1);
     const int64_t off = (src * a.s_row + (valid ? j : 0) * a.s_pos) * 2;  // bytes; invalid lanes read key 0
     u32x4_t kx[kWave / 4], vx[kWave / 4];
@@ -1532,6 +1535,9 @@ __global__ __launch_bounds__(256) void beam_gen_kernel_d512(BeamGenArgs a) {
   __shared__ float s_m[NW], s_l[NW];
   const int h = blockIdx.x, r = blockIdx.y;
   const int tid = threadIdx.x, w = tid / kWave, lane = tid - w * kWave;
+  // This wave's first 16 keys' row pointers load beside the length (index clamped into the row's capacity).
+  const int jf = KW * w + (lane & (KW - 1));
+  const int32_t ptr0 = a.ptr[(int64_t)r * a.ptr_stride + (jf < a.gen_cap ? jf : a.gen_cap - 1)];
   const int64_t n = clamp64(a.gen_len[r], 0, a.gen_cap);
   float qv[8];
   {
@@ -1549,7 +1555,7 @@ __global__ __launch_bounds__(256) void beam_gen_kernel_d512(BeamGenArgs a) {
     const int64_t jb = j0 + KW * w;  // this wave's first key
     const int64_t j = jb + (lane & (KW - 1));
     const bool valid = j < n;
-    int64_t src = valid ? (int64_t)a.ptr[(int64_t)r * a.ptr_stride + j] : 0;
+    int64_t src = valid ? (j0 == 0 ? (int64_t)ptr0 : (int64_t)a.ptr[(int64_t)r * a.ptr_stride + j]) : 0;
     src = clamp64(src, 0, a.gen_rows - 1);
     const int64_t off = (src * a.s_row + (valid ? j : 0) * a.s_pos) * 2;  // bytes; invalid keys read key 0
     u32x4_t kx[KW], vx[KW];
