@@ -113,6 +113,31 @@ int omni_verify_attention(const void *q, const void *k_cache, const void *v_cach
                           void *out, void *workspace, size_t workspace_bytes, int32_t *counters,
                           int32_t flags, int32_t dtype, void *stream);
 
+/* Capacity of the static scratch behind omni_verify_attention_static. */
+#define OMNI_STATIC_WORKSPACE_BYTES ((size_t)32 << 20) /* split partials: 32 MiB per GPU */
+#define OMNI_STATIC_MAX_UNITS 16384                    /* rows * heads (merge tickets) */
+
+/*
+ * omni_verify_attention without a caller's workspace or tickets: it allocates nothing (no hipMalloc, no
+ * allocating library call), for callers that cannot allocate -- code under HIP graph capture that must not
+ * call hipMalloc, tight serving loops, harnesses that forbid allocation.  No counterpart in the reference
+ * (its Triton wrappers allocate their split workspace with torch.empty on every call, kernels.py:349-350).
+ *
+ * Arguments and results are those of omni_verify_attention with workspace, workspace_bytes and counters
+ * taken away: the split partials and merge tickets live in a file-scope device array of the library
+ * (OMNI_STATIC_WORKSPACE_BYTES of partials plus OMNI_STATIC_MAX_UNITS tickets), one copy per GPU, held
+ * until the process ends.  A shape whose workspace (omni_verify_attention_workspace) exceeds
+ * OMNI_STATIC_WORKSPACE_BYTES, or with rows * heads > OMNI_STATIC_MAX_UNITS, returns OMNI_ERR_WORKSPACE
+ * before anything is launched.  Each call first clears the tickets with a fill kernel on ``stream``, then
+ * launches what omni_verify_attention launches.  Every call on a GPU shares that GPU's array: calls that
+ * overlap in time on one GPU (other streams, other threads) race and must not be made.
+ */
+int omni_verify_attention_static(const void *q, const void *k_cache, const void *v_cache,
+                                 int64_t stride_row, int64_t stride_head, int64_t stride_pos,
+                                 int64_t cache_len, const int64_t *lengths, int32_t rows, int32_t tokens,
+                                 int32_t heads, int32_t head_dim, int32_t keys, int32_t chunk, float scale,
+                                 void *out, int32_t flags, int32_t dtype, void *stream);
+
 /* Bytes of workspace omni_beam_attention needs for this shape and split size (0: default). */
 size_t omni_beam_attention_workspace(int32_t groups, int32_t beams, int32_t heads, int32_t head_dim,
                                      int32_t ctx_keys, int32_t chunk);

@@ -20,6 +20,8 @@ OK = 0
 F32, BF16 = 0, 1
 ATTN_SEPARATE_COMBINE = 1
 ATTN_SPLIT_K = 2
+STATIC_WORKSPACE_BYTES = 32 << 20  # OMNI_STATIC_WORKSPACE_BYTES
+STATIC_MAX_UNITS = 16384  # OMNI_STATIC_MAX_UNITS
 
 _P = c_void_p
 _SIGNATURES = {
@@ -32,6 +34,8 @@ _SIGNATURES = {
     "omni_verify_attention": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, c_int32, c_int32, c_int32,
                                       c_int32, c_int32, c_int32, c_float, _P, _P, c_size_t, _P, c_int32, c_int32,
                                       _P]),
+    "omni_verify_attention_static": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, c_int32, c_int32,
+                                             c_int32, c_int32, c_int32, c_int32, c_float, _P, c_int32, c_int32, _P]),
     "omni_beam_attention_workspace": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
     "omni_beam_attention": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, c_int64, c_int64,
                                     c_int64, c_int64, c_int64, _P, c_int64, _P, c_int32, c_int32, c_int32, c_int32,

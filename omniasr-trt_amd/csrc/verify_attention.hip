@@ -30,6 +30,8 @@
 // keys through pointers) is at the end of the file.
 #include <math.h>
 
+#include <mutex>
+
 #include "attn_tiles.h"
 #include "common.h"
 
@@ -1311,6 +1313,79 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
   st = launch_attention(a, rows, dtype, s);
   if (st != OMNI_OK || !a.separate) return st;
   return launch_combine(a, rows, dtype, s);
+}
+
+// ---------------------------------------------------------------------------------------------- static scratch
+
+// The verify attention for callers that cannot allocate: its split partials and merge tickets live in this
+// file-scope array, one copy per GPU for the life of the process.  Host code never passes ``scratch`` itself to
+// a kernel (on the host the name is a stand-in, not a device address): it passes the device address that
+// hipGetSymbolAddress returns for the current device, looked up once per device and kept in g_scratch.
+static __device__ __align__(256) unsigned char scratch[OMNI_STATIC_WORKSPACE_BYTES +
+                                                       OMNI_STATIC_MAX_UNITS * sizeof(int32_t)];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxDevices];
+
+// This device's copy of ``scratch`` (looked up on the first call made with the device current).
+int scratch_address(void** ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return OMNI_ERR_INVALID;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (p == nullptr) return OMNI_ERR_INVALID;
+    g_scratch[dev] = p;
+  }
+  *ptr = g_scratch[dev];
+  return OMNI_OK;
+}
+
+__global__ __launch_bounds__(256) void zero_tickets_kernel(int32_t* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+}  // namespace
+
+extern "C" int omni_verify_attention_static(const void* q, const void* k_cache, const void* v_cache,
+                                            int64_t stride_row, int64_t stride_head, int64_t stride_pos,
+                                            int64_t cache_len, const int64_t* lengths, int32_t rows,
+                                            int32_t tokens, int32_t heads, int32_t head_dim, int32_t keys,
+                                            int32_t chunk, float scale, void* out, int32_t flags, int32_t dtype,
+                                            void* stream) {
+  // The checks omni_verify_attention makes on its own arguments come first, so that this entry point answers a
+  // bad shape with the same status.
+  if (rows < 0 || keys <= 0 || cache_len <= 0) return OMNI_ERR_INVALID;
+  int st = check_attention_shape(tokens, heads, head_dim, dtype, scale, stride_pos);
+  if (st != OMNI_OK) return st;
+  if (rows == 0) return OMNI_OK;
+  if (chunk == 0) chunk = omni_verify_attention_chunk(rows, tokens, heads, head_dim, keys);
+  if (chunk <= 0 || chunk % 32 != 0) return OMNI_ERR_INVALID;
+  const size_t need = omni_verify_attention_workspace(rows, tokens, heads, head_dim, keys, chunk);
+  const int64_t units = (int64_t)rows * heads;
+  if (need > OMNI_STATIC_WORKSPACE_BYTES || units > OMNI_STATIC_MAX_UNITS) return OMNI_ERR_WORKSPACE;
+  void* base = nullptr;
+  st = scratch_address(&base);
+  if (st != OMNI_OK) return st;
+  int32_t* tickets = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(base) + OMNI_STATIC_WORKSPACE_BYTES);
+  // The tickets must be zero when the attention starts.  Every call leaves them zero, but the array keeps whatever
+  // the last call on this GPU left, so they are cleared here by a kernel (a fill kernel, not hipMemsetAsync, so
+  // that a captured graph replays it correctly).
+  hipStream_t s = (hipStream_t)stream;
+  const int n = (int)units;
+  zero_tickets_kernel<<<(n + 255) / 256, 256, 0, s>>>(tickets, n);
+  st = omni_launch_status();
+  if (st != OMNI_OK) return st;
+  return omni_verify_attention(q, k_cache, v_cache, stride_row, stride_head, stride_pos, cache_len, lengths, rows,
+                               tokens, heads, head_dim, keys, chunk, scale, out, base, OMNI_STATIC_WORKSPACE_BYTES,
+                               tickets, flags, dtype, stream);
 }
 
 // ---------------------------------------------------------------------------------------------- beams

@@ -153,6 +153,35 @@ def _verify(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengt
     return out
 
 
+def verify_attention_static(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor,
+                            tokens: int, keys: int, scale: float, out: torch.Tensor, chunk: int = 0,
+                            separate: bool = True, split_k: bool = False) -> torch.Tensor:
+    """:func:`draft_attention` into the caller's ``out`` (same shape and dtype as ``q``) with nothing allocated: the
+    library's per-GPU static scratch holds the split partials and tickets (``omni_verify_attention_static``).  Shapes
+    whose workspace exceeds ``_lib.STATIC_WORKSPACE_BYTES`` (or with rows x heads > ``_lib.STATIC_MAX_UNITS``) raise.
+    Calls that overlap in time on one GPU race: they share its scratch."""
+    lib = _lib.load()
+    rows_total, heads, dim = q.shape
+    _need(rows_total % tokens == 0, "q: [B*T, H, D]")
+    groups = rows_total // tokens
+    _need(q.is_contiguous(), "q: contiguous [B*T, H, D]")
+    _need(out.shape == q.shape and out.dtype == q.dtype and out.is_contiguous() and out.device == q.device,
+          "out: contiguous, q's shape, dtype and device")
+    _need(k_cache.dtype == q.dtype == v_cache.dtype, "q and the caches: one dtype")
+    _need(k_cache.stride() == v_cache.stride() and k_cache.shape == v_cache.shape, "k_cache / v_cache: same layout")
+    _need(k_cache.dim() == 4 and k_cache.stride(3) == 1 and k_cache.size(3) == dim, "caches: [>=B, H, S, D]")
+    _need(k_cache.size(0) >= groups and k_cache.size(1) == heads, "caches: at least B rows of H heads")
+    _index(lengths, "lengths")
+    _need(lengths.numel() >= groups, "lengths: [B]")
+    flags = (_lib.ATTN_SEPARATE_COMBINE if separate else 0) | (_lib.ATTN_SPLIT_K if split_k else 0)
+    status = lib.omni_verify_attention_static(
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1),
+        k_cache.stride(2), k_cache.size(2), lengths.data_ptr(), groups, tokens, heads, dim, keys, int(chunk or 0),
+        float(scale), out.data_ptr(), flags, _dtype(q), _stream(q))
+    _lib.check(status, "verify attention (static scratch)")
+    return out
+
+
 def draft_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor,
                     tokens: int, keys: int, scale: float, **launch) -> torch.Tensor:
     """Draft verification: ``q`` [B*T, H, D], row b's T queries at rows b*T .. b*T+T-1; query i of row b attends to

@@ -99,3 +99,18 @@ def test_kernels_refuse_without_gpu():
     with pytest.raises(Exception):
         kernels.rope_kv(torch.zeros(1, 48), torch.zeros(8, 4, 2), torch.zeros(1, dtype=torch.long),
                         torch.zeros(1, 4, 8, 8), torch.zeros(1, 4, 8, 8), 2)
+
+
+def test_static_scratch_refuses_oversized_shapes_before_launch():
+    """omni_verify_attention_static: a shape whose workspace exceeds the static scratch, or with more (row, head)
+    units than it has tickets, is refused with OMNI_ERR_WORKSPACE before anything is looked up or launched."""
+    lib = _lib.load()
+    assert lib.omni_verify_attention_workspace(8, 16, 32, 128, 8192, 64) > _lib.STATIC_WORKSPACE_BYTES
+    args = [FAKE, FAKE, FAKE, 1 << 20, 1 << 16, 128, 8192, FAKE, 8, 16, 32, 128, 8192, 64, 0.1, FAKE, 0, _lib.BF16,
+            None]
+    assert lib.omni_verify_attention_static(*args) == -4
+    args[8], args[9], args[10], args[11], args[12], args[13] = 1024, 1, 32, 16, 256, 256  # 32768 units > 16384
+    assert lib.omni_verify_attention_workspace(1024, 1, 32, 16, 256, 256) < _lib.STATIC_WORKSPACE_BYTES
+    assert lib.omni_verify_attention_static(*args) == -4
+    args[9] = 17  # the shape checks of omni_verify_attention come first
+    assert lib.omni_verify_attention_static(*args) == -3
