@@ -314,10 +314,7 @@ def beam_leg(pkg, torch, w: Workload, steps: int, warmup: int, reps: int) -> dic
     lengths = rng.integers(750, 2401, SLOTS)
     g = torch.Generator(device="cuda").manual_seed(1006)
     ctxs = [torch.randn(int(n), w.cfg.model_dim, device="cuda", generator=g).to(torch.bfloat16) for n in lengths]
-    dec.gdone[:] = True
-    dec.k_step[:] = 1
-    dec.tok.zero_()
-    beam._Groups(dec, SLOTS, iter(()), None, None).fill([(i, i, c) for i, c in enumerate(ctxs)])
+    dec.start_groups(ctxs)
     dec.ensure_beam(dec.ccap, warmup + steps + 4)
     ckeys = min(dec.ccap, beam.bucket(int(lengths.max())))
     run = dec.beam_runner(SLOTS, ckeys)

@@ -1,24 +1,24 @@
 """Batched beam search of the omniASR LLM decoder on MI355X: every input's search as the reference runs it at batch 1.
 
-Rules of the reference's ``BeamDecoder`` (src/omniasr_trt/beam.py) and its batch-1 loop ``beam_reference``
-(src/omniasr_trt/llm.py:205-254): an input (a "group" of ``beams`` rows) starts from the ``beams`` best first
-tokens; every step each row offers score + log p for every token (``length_norm``: the running mean, switched on
-by the group's row 0), a finished row only EOS at its frozen score; the best ``beams`` offers of the group survive
-and the rows follow their parents; the repetition stop ends a row at the exact step it fires; the text is row 0's
-once every row has finished or the position cap is reached.
+The search of the reference's ``BeamDecoder`` (src/omniasr_trt/beam.py) and of its batch-1 loop ``beam_reference``
+(src/omniasr_trt/llm.py:205-254): an input is a *group* of ``beams`` rows that starts from the ``beams`` best first
+tokens.  At each step every row offers score + log p for every token (with ``length_norm`` the running mean of its
+log-probabilities, used once the group's row 0 has a token), a finished row offers only EOS at its frozen score; the
+group keeps its ``beams`` best offers, each row taking over its parent's history; the repetition stop ends a row at
+the exact step it fires; the text is row 0's once every row has finished or the position cap is reached.
 
-Memory layout (HBM):
+Memory (HBM):
 
-* ``kc`` / ``vc`` [layers, groups, H, C, Dh]: each input's context, prefilled once and shared by its beams;
-* ``kg`` / ``vg`` [layers, rows, H, G, Dh]: the K/V of the token row r fed at generated position j, written once
-  at (r, j); ``ptr[r, j]`` (int32) names the row that wrote position j of r's history, so following a parent
-  copies pointers and the token history ``hist``, never K/V;
-* ``kernels.beam_attention`` reads a group's context once for all of its beams (the verify kernel's MFMA tiles,
-  beams as its queries), then each row's generated keys through ``ptr``.
+* ``kc`` / ``vc`` [layers, groups, H, C, Dh]: each input's context, prefilled once for all of its beams;
+* ``kg`` / ``vg`` [layers, rows, H, G, Dh]: the K/V of the token row r fed at generated position j, written once at
+  (r, j); ``ptr[r, j]`` (int32) names the row whose K/V is position j of r's history, so taking over a parent's
+  history copies pointers and token ids (``hist``), never K/V;
+* ``kernels.beam_attention`` reads a group's context once for all of its beams (the beams are the queries of the
+  verify kernel's tiles), then each row's generated keys through its pointers.
 
-One step (the layers, the LM head, the per-group top-k over beams x vocabulary, the pointer gathers) is one HIP
-graph per (groups, context bucket); the host looks every ``sync_every`` steps, or at the exact step a group's
-repetition check is due.
+One step (layers, LM head, per-group top-k over beams x vocabulary, the history reorder) is one HIP graph per
+(groups, context bucket); the host looks every ``sync_every`` steps, or at the exact step a group's repetition check
+is due.
 """
 
 from __future__ import annotations
@@ -26,16 +26,25 @@ from __future__ import annotations
 import numpy as np
 import torch
 import torch.nn.functional as F
+from torch import Tensor
 
 from . import kernels
-from .decode import KEY_BUCKET, LIMIT, GreedyDecoder
+from .batching import UnitScheduler
+from .decode import KEY_BUCKET, LIMIT, GreedyDecoder, _regrown
 from .llm import BOS, CHECK_EVERY, CHECK_RATIO, CHECK_WINDOW, EOS, MAX_GEN, PAD, compression_ratio
 from .modeling import DecoderModel
 
 
 def bucket(n: int) -> int:
-    """``n`` rounded up to the graph bucket (at least one bucket)."""
+    """``n`` rounded up to the graph bucket, at least one bucket (read at call time, so tests may shrink it)."""
     return -(-max(int(n), 1) // KEY_BUCKET) * KEY_BUCKET
+
+
+def next_check(k: int, ctx_len: int) -> int:
+    """The first step index >= k whose chosen token sits at a checked position: input position ctx_len - 1 + k a
+    multiple of ``CHECK_EVERY`` and beyond ctx_len + ``CHECK_WINDOW`` (src/omniasr_trt/llm.py:243-246)."""
+    k = max(k, CHECK_WINDOW + 2)
+    return k + (-(ctx_len - 1 + k)) % CHECK_EVERY
 
 
 class BeamDecoder(GreedyDecoder):
@@ -44,7 +53,7 @@ class BeamDecoder(GreedyDecoder):
 
     def __init__(self, model: DecoderModel, *, beams: int, length_norm: bool = False, max_batch: int = 8,
                  sync_every: int = 16, graphs: bool = True, reserve: int = 512, fused: bool = True):
-        if beams < 1 or beams > 16:
+        if not 1 <= beams <= 16:
             raise ValueError("beams: 1..16")
         super().__init__(model, max_batch=max_batch * beams, sync_every=sync_every, graphs=graphs, reserve=reserve,
                          fused=fused)
@@ -52,51 +61,47 @@ class BeamDecoder(GreedyDecoder):
         self.length_norm = length_norm
         self.groups = max_batch
         rows, dev = max_batch * beams, self.device
-        # Scores as the reference keeps them: fp32, or the model's dtype if that is wider.
-        self.score = torch.zeros(rows, device=dev, dtype=torch.promote_types(torch.float32, self.dtype))
-        self.ended = torch.ones(rows, device=dev, dtype=torch.bool)
-        self.count = torch.zeros(rows, device=dev, dtype=torch.long)  # tokens other than PAD / EOS (length_norm)
-        self.rows = torch.arange(rows, device=dev)
-        self.group = self.rows // beams
-        self.lead = self.group * beams  # row 0 of each row's group
-        self.k_step = torch.zeros(max_batch, device=dev, dtype=torch.long)  # tokens chosen in the current context
-        self.ctx = torch.ones(max_batch, device=dev, dtype=torch.long)  # its length
-        self.gdone = torch.ones(max_batch, device=dev, dtype=torch.bool)
+        # Row state.  Scores in fp32 as the reference keeps them (fp64 for an fp64 model).
+        self.score = torch.zeros(rows, dtype=torch.promote_types(torch.float32, self.dtype), device=dev)
+        self.ended = torch.ones(rows, dtype=torch.bool, device=dev)
+        self.count = torch.zeros(rows, dtype=torch.long, device=dev)  # tokens other than PAD / EOS (length_norm)
+        self.row_ids = torch.arange(rows, device=dev)
+        # Group state: tokens chosen in the current context, the context's length, finished.
+        self.k_step = torch.zeros(max_batch, dtype=torch.long, device=dev)
+        self.ctx = torch.ones(max_batch, dtype=torch.long, device=dev)
+        self.gdone = torch.ones(max_batch, dtype=torch.bool, device=dev)
         self.kc = self.vc = self.kg = self.vg = self.ptr = self.hist = None
         self.ccap = self.gcap = 0
+        self._normal_caps: tuple[int, int] | None = None
         self.stats["repetition_stops"] = 0
 
     # ------------------------------------------------------------------ buffers
 
     def ensure_beam(self, ctx_len: int, gen_len: int) -> None:
-        """Context caches for ``ctx_len`` positions per input; generated caches, pointers and histories for
-        ``gen_len`` positions per row (contents kept when they grow; graphs are captured again)."""
-        ctx_len, gen_len = bucket(ctx_len), min(bucket(gen_len), bucket(MAX_GEN))
-        if ctx_len <= self.ccap and gen_len <= self.gcap:
+        """Context caches for ``ctx_len`` positions per input, generated caches / pointers / histories for
+        ``gen_len`` positions per row (both rounded up to the bucket); growing keeps the contents and drops the
+        graphs."""
+        want_c, want_g = bucket(ctx_len), min(bucket(gen_len), bucket(MAX_GEN))
+        grow_c, grow_g = want_c > self.ccap, want_g > self.gcap
+        if not (grow_c or grow_g):
             return
         torch.cuda.synchronize(self.device)
-        layers, heads, dh, dt, dev = len(self.layers), self.heads, self.head_dim, self.dtype, self.device
-        if ctx_len > self.ccap:
-            kc = torch.zeros(layers, self.groups, heads, ctx_len, dh, device=dev, dtype=dt)
-            vc = torch.zeros_like(kc)
-            if self.ccap:
-                kc[..., : self.ccap, :] = self.kc
-                vc[..., : self.ccap, :] = self.vc
-                self.stats["grows"] += 1
-            self.kc, self.vc, self.ccap = kc, vc, ctx_len
-        if gen_len > self.gcap:
+        layers, dev, dt = len(self.layers), self.device, self.dtype
+        if grow_c:
+            shape = (layers, self.groups, self.heads, want_c, self.head_dim)
+            self.kc = _regrown(self.kc, shape, 3, 0, dt, dev)
+            self.vc = _regrown(self.vc, shape, 3, 0, dt, dev)
+            self.stats["grows"] += bool(self.ccap)
+            self.ccap = want_c
+        if grow_g:
             rows = self.groups * self.beams
-            kg = torch.zeros(layers, rows, heads, gen_len, dh, device=dev, dtype=dt)
-            vg = torch.zeros_like(kg)
-            ptr = torch.zeros(rows, gen_len, device=dev, dtype=torch.int32)
-            hist = torch.full((rows, gen_len + 1), PAD, device=dev, dtype=torch.int32)
-            if self.gcap:
-                kg[..., : self.gcap, :] = self.kg
-                vg[..., : self.gcap, :] = self.vg
-                ptr[:, : self.gcap] = self.ptr
-                hist[:, : self.gcap + 1] = self.hist
-                self.stats["grows"] += 1
-            self.kg, self.vg, self.ptr, self.hist, self.gcap = kg, vg, ptr, hist, gen_len
+            shape = (layers, rows, self.heads, want_g, self.head_dim)
+            self.kg = _regrown(self.kg, shape, 3, 0, dt, dev)
+            self.vg = _regrown(self.vg, shape, 3, 0, dt, dev)
+            self.ptr = _regrown(self.ptr, (rows, want_g), 1, 0, torch.int32, dev)
+            self.hist = _regrown(self.hist, (rows, want_g + 1), 1, PAD, torch.int32, dev)
+            self.stats["grows"] += bool(self.gcap)
+            self.gcap = want_g
         self.reset_graphs()
 
     def release(self) -> None:
@@ -107,89 +112,87 @@ class BeamDecoder(GreedyDecoder):
 
     # ------------------------------------------------------------------ one step
 
-    def beam_state(self) -> list[torch.Tensor]:
-        """What a step changes besides the caches (restored after the warm-up step of a capture)."""
+    def beam_state(self) -> list[Tensor]:
+        """What a step changes besides the caches."""
         return [self.tok, self.score, self.ended, self.count, self.k_step, self.gdone, self.hist, self.ptr]
+
+    def _offers(self, logp: Tensor, r: int) -> Tensor:
+        """Every row's offer for every token [R, V]: score + log p (``length_norm``: the mean over the row's tokens,
+        once the group's row 0 has one), -inf for a finished row except EOS at its frozen score."""
+        score, count, ended = self.score[:r, None], self.count[:r, None], self.ended[:r]
+        summed = score + logp
+        if self.length_norm:
+            lead_count = count.view(-1, self.beams)[:, :1].expand(-1, self.beams).reshape(-1, 1)
+            summed = torch.where(lead_count > 0, (score * count + logp) / (count + 1), summed)
+        offers = summed.masked_fill(ended[:, None], float("-inf"))
+        offers[:, EOS] = torch.where(ended, self.score[:r], offers[:, EOS])
+        return offers
 
     def step_beam(self, s: int, ckeys: int) -> None:
         """One step of groups 0..s-1 (rows 0..s*N-1), in place; finished groups keep their state.
         (src/omniasr_trt/beam.py:127-187)"""
-        m, n = self.m, self.beams
-        r = s * n
-        tok, score, ended, count = self.tok[:r], self.score[:r], self.ended[:r], self.count[:r]
-        k_step, ctx, gdone = self.k_step[:s], self.ctx[:s], self.gdone[:s]
-        hist, ptr, rows, group = self.hist[:r], self.ptr[:r], self.rows[:r], self.group[:r]
-        live = ~gdone[group]
-        k = k_step[group]  # the token in ``tok`` is hist[r, k - 1]
-        pos = ctx[group] - 1 + k  # its input position
-        j = (k - 1).clamp(min=0)  # its generated cache position
-        ctx_len = torch.where(gdone, 0, ctx)
-        gen_len = torch.where(live, k, 0)
-        # Position j is written by this row in this step, and this step's attention reads it through ``ptr``.
-        col = j[:, None]
-        ptr.scatter_(1, col, torch.where(live[:, None], rows[:, None].to(ptr.dtype), ptr.gather(1, col)))
-        h = m.text_frontend.weight[tok]
+        n, r = self.beams, s * self.beams
+        group_done = self.gdone[:s]
+        live = ~group_done.repeat_interleave(n)  # [R]
+        k = self.k_step[:s].repeat_interleave(n)  # the token in ``tok`` is hist[row, k - 1]
+        rows = self.row_ids[:r]
+        tok, ptr, hist = self.tok[:r], self.ptr[:r], self.hist[:r]
+        pos = self.ctx[:s].repeat_interleave(n) + k - 1  # input position of ``tok``
+        gen_pos = (k - 1).clamp(min=0)  # its generated cache position
+        ctx_len = self.ctx[:s].masked_fill(group_done, 0)
+        gen_len = k.masked_fill(~live, 0)
+        # A live row writes generated position gen_pos in this step, and this step's attention reads it already:
+        # its pointer there names the row itself.
+        here = gen_pos[:, None]
+        ptr.scatter_(1, here, torch.where(live[:, None], rows[:, None].to(ptr.dtype), ptr.gather(1, here)))
         scale = self.head_dim ** -0.5
-        for i, layer in enumerate(m.llama_decoder.layers):
-            qkv_w, out_w, gi_w, ffo_w = self.layers[i]
-            qkv = layer.self_attn_layer_norm(h) @ qkv_w.t()
-            q = kernels.rope_kv(qkv, m.rope, pos, self.kg[i], self.vg[i], self.heads, None, j)
-            o = kernels.beam_attention(q, self.kc[i], self.vc[i], ctx_len, self.kg[i], self.vg[i], ptr, gen_len, n,
-                                       ckeys, scale).reshape(r, -1)
-            h.addmm_(o, out_w.t())  # in place: the GEMM adds into the residual, no copy of it
-            gate, inner = (layer.ffn_layer_norm(h) @ gi_w.t()).chunk(2, -1)
-            h.addmm_(inner * F.silu(gate), ffo_w.t())
-        logp = F.log_softmax(m.final_proj(m.llama_decoder.layer_norm(h)), dim=-1)  # [R, V], model dtype
+        h = self.m.text_frontend.weight[tok]
+        for i in range(len(self.layers)):
+            kg, vg = self.kg[i], self.vg[i]
+
+            def attend(qkv, i=i, kg=kg, vg=vg):
+                q = kernels.rope_kv(qkv, self.m.rope, pos, kg, vg, self.heads, None, gen_pos)
+                return kernels.beam_attention(q, self.kc[i], self.vc[i], ctx_len, kg, vg, ptr, gen_len, n, ckeys,
+                                              scale).reshape(r, -1)
+
+            self._layer(i, h, attend)
+        logp = F.log_softmax(self._head(h), dim=-1)  # [R, V], model dtype
         vocab = logp.size(-1)
-        if self.length_norm:
-            c = count[:, None]
-            mean = (score[:, None] * c + logp) / (c + 1)
-            cand = torch.where(count[self.lead[:r]][:, None] > 0, mean, score[:, None] + logp)
-        else:
-            cand = score[:, None] + logp
-        cand = cand.masked_fill(ended[:, None], float("-inf"))
-        cand[:, EOS] = torch.where(ended, score, cand[:, EOS])
-        top, pick = cand.view(s, n * vocab).topk(n, dim=-1, sorted=True)  # [S, N], best first
-        parent = torch.where(live, (pick // vocab + self.lead[:r].view(s, n)[:, :1]).view(-1), rows)
-        new = torch.where(live, (pick % vocab).view(-1), tok)
-        ptr.copy_(ptr[parent])
-        hist.copy_(hist[parent])
-        p_ended, p_score, p_count = ended[parent], score[parent], count[parent]
-        new = torch.where(p_ended, EOS, new)
+        best, flat = self._offers(logp, r).view(s, n * vocab).topk(n, dim=-1, sorted=True)  # [S, N], best first
+        lead = (torch.arange(s, device=self.device) * n)[:, None]
+        parent = torch.where(live, (flat // vocab + lead).view(-1), rows)
+        chosen = torch.where(live, (flat % vocab).view(-1), tok)
+        self._take_over(parent, chosen, best.view(-1), live, k, r)
+        self.k_step[:s] += (~group_done).long()
+        ended_groups = self.ended[:r].view(s, n).all(-1)
+        group_done |= ended_groups | (self.ctx[:s] + self.k_step[:s] - 2 >= LIMIT)
+
+    def _take_over(self, parent: Tensor, chosen: Tensor, best: Tensor, live: Tensor, k: Tensor, r: int) -> None:
+        """Each row r becomes a copy of ``parent[r]`` (history, pointers, score, count, finished) extended by
+        ``chosen[r]`` (EOS when the parent had finished) at step k; live rows whose parent was still open take the
+        offer ``best[r]`` as their score."""
+        ptr, hist = self.ptr[:r], self.hist[:r]
+        ptr.copy_(ptr.index_select(0, parent))
+        hist.copy_(hist.index_select(0, parent))
+        was_ended = self.ended[:r].index_select(0, parent)
+        was_score = self.score[:r].index_select(0, parent)
+        was_count = self.count[:r].index_select(0, parent)
+        chosen = chosen.masked_fill(was_ended, EOS)
         col = k[:, None]
-        hist.scatter_(1, col, torch.where(live[:, None], new[:, None].to(hist.dtype), hist.gather(1, col)))
-        grows = live & ~p_ended
-        score.copy_(torch.where(grows, top.view(-1), p_score))
-        count.copy_(p_count + (grows & (new != PAD) & (new != EOS)).long())
-        ended.copy_(torch.where(live, new == EOS, p_ended))
-        tok.copy_(new)
-        k_step.add_((~gdone).long())
-        gdone |= ended.view(s, n).all(-1) | (ctx - 2 + k_step >= LIMIT)
+        hist.scatter_(1, col, torch.where(live[:, None], chosen[:, None].to(hist.dtype), hist.gather(1, col)))
+        extends = live & ~was_ended
+        self.score[:r] = torch.where(extends, best, was_score)
+        self.count[:r] = was_count + (extends & (chosen != PAD) & (chosen != EOS)).long()
+        self.ended[:r] = torch.where(live, chosen == EOS, was_ended)
+        self.tok[:r] = chosen
 
     def beam_runner(self, s: int, ckeys: int):
-        """The step of groups 0..s-1 with ``ckeys`` context positions in reach: a replayed HIP graph per (s, ckeys)
-        (the generated keys' loop bound is read on the device, so it needs no bucket)."""
-        if not self.use_graphs:
-            return lambda: self.step_beam(s, ckeys)
-        key = ("beam", s, ckeys)
-        if key not in self.graphs:
-            torch.cuda.synchronize(self.device)
-            saved = [t.clone() for t in self.beam_state()]
-            stream = self.capture_stream
-            stream.wait_stream(torch.cuda.current_stream(self.device))
-            with torch.cuda.stream(stream):
-                self.step_beam(s, ckeys)  # warm-up; the K/V it writes are written again, identically, by the replay
-                for t, v in zip(self.beam_state(), saved, strict=True):
-                    t.copy_(v)
-                graph = torch.cuda.CUDAGraph()
-                graph.capture_begin(pool=self.pool)
-                self.step_beam(s, ckeys)
-                graph.capture_end()
-            torch.cuda.current_stream(self.device).wait_stream(stream)
-            torch.cuda.synchronize(self.device)
-            self.graphs[key] = graph
-            self.stats["captures"] += 1
-        return self.graphs[key].replay
+        """The step of groups 0..s-1 with ``ckeys`` context positions in reach, as a callable (a graph replay per
+        (s, ckeys); the generated keys' count is read on the device, so it needs no bucket)."""
+        before = self.graphs.captures
+        run = self.graphs.runner(("beam", s, ckeys), lambda: self.step_beam(s, ckeys), self.beam_state)
+        self.stats["captures"] += self.graphs.captures - before
+        return run
 
     # ------------------------------------------------------------------ streams
 
@@ -197,123 +200,107 @@ class BeamDecoder(GreedyDecoder):
     def decode_streams(self, n_streams: int, start, advance) -> None:
         """As ``GreedyDecoder.decode_streams``; ``advance(j, tokens)`` receives the best beam's tokens.
         (src/omniasr_trt/beam.py:215-315)"""
-        _Groups(self, min(self.groups, n_streams), iter(range(n_streams)), start, advance).run()
+        s = min(self.groups, n_streams)
+        self.gdone[:s] = True
+        self.k_step[:s] = 1
+        self.tok[: s * self.beams] = 0
+        self._normal_caps = None
+        UnitScheduler(s, n_streams, start, advance, admit=self.admit,
+                      finished=lambda: np.flatnonzero(self.gdone[:s].cpu().numpy()).tolist(),
+                      harvest=self._best_tokens, run_block=self._run_block, retire=self._retire).run()
 
+    @torch.inference_mode()
+    def start_groups(self, ctxs: list[Tensor]) -> None:
+        """Prefill ``ctxs`` into groups 0..len-1 and start their searches, for callers that then drive
+        :meth:`beam_runner` by hand (benchmarks)."""
+        s = len(ctxs)
+        self.gdone[:s] = True
+        self.k_step[:s] = 1
+        self.tok[: s * self.beams] = 0
+        self._normal_caps = None
+        sched = UnitScheduler(s, s, ctxs.__getitem__, lambda j, tokens: None, admit=self.admit, finished=list,
+                              harvest=self._best_tokens, run_block=lambda sched: None)
+        sched.assign([(g, g, c) for g, c in enumerate(ctxs)])
 
-class _Groups:
-    """Host side of ``BeamDecoder.decode_streams``: the stream each group decodes, the checks due."""
-
-    def __init__(self, dec: BeamDecoder, s: int, upcoming, start, advance):
-        self.dec, self.s = dec, s
-        self.upcoming, self.start, self.advance = upcoming, start, advance
-        self.stream = np.full(s, -1)
-        self.ctx_len = np.zeros(s, dtype=np.int64)
-        self.normal: tuple[int, int] | None = None
-
-    def fill(self, pairs: list) -> None:
-        """Prefill ``pairs`` [(group, stream, context)]; each group starts from its context's N best tokens."""
-        dec, n = self.dec, self.dec.beams
-        refilled = {g for g, _, _ in pairs}
-        k_now = dec.k_step[: self.s].cpu().numpy()
-        busy = [int(k_now[g]) for g in range(self.s) if self.stream[g] >= 0 and g not in refilled]
-        longest = max(c.size(0) for _, _, c in pairs)
-        dec.ensure_beam(max(dec.context_floor, int(self.ctx_len.max()), longest),
-                        max([dec.reserve] + [k + dec.sync_every + 2 for k in busy]))
-        self.normal = self.normal or (dec.ccap, dec.gcap)
+    def admit(self, sched: UnitScheduler, pairs: list) -> None:
+        """Prefill ``[(group, stream, context)]`` into their groups' context caches; each group starts from its
+        context's ``beams`` most likely first tokens (one live hypothesis at the first step)."""
+        n = self.beams
         groups = [g for g, _, _ in pairs]
-        with dec.phase("prefill"):
-            logp = dec.prefill_into([c for _, _, c in pairs], groups, dec.kc, dec.vc)  # [b, V]
-        dec.check("prefill")
-        top, first = logp.to(dec.score.dtype).topk(n, dim=-1)  # only one live beam at the first step
-        idx = torch.tensor(groups, device=dec.device)
-        rows = (idx[:, None] * n + torch.arange(n, device=dec.device)).view(-1)
-        first = first.view(-1)
-        dec.tok[rows] = first
-        dec.score[rows] = top.view(-1)
-        dec.ended[rows] = first == EOS
-        dec.count[rows] = ((first != PAD) & (first != EOS)).long()
-        dec.hist[rows, 0] = first.to(torch.int32)
-        lens = torch.tensor([c.size(0) for _, _, c in pairs], device=dec.device)
-        dec.k_step[idx] = 1
-        dec.ctx[idx] = lens
-        dec.gdone[idx] = dec.ended[rows].view(-1, n).all(-1) | (lens - 1 >= LIMIT)
-        for g, j, c in pairs:
-            self.stream[g], self.ctx_len[g] = j, c.size(0)
+        ctxs = [c for _, _, c in pairs]
+        others = [g for g in sched.active() if g not in set(groups)]
+        gen_need = self.reserve
+        if others:  # groups still decoding keep room for a whole block of steps
+            steps = self.k_step[torch.tensor(others, device=self.device)]
+            gen_need = max(gen_need, int(steps.max()) + self.sync_every + 2)
+        longest = max(a.ctx_len for a in sched.assigned if a is not None)
+        self.ensure_beam(max(self.context_floor, longest), gen_need)
+        if self._normal_caps is None:
+            self._normal_caps = (self.ccap, self.gcap)
+        with self.phase("prefill"):
+            logp = self.prefill_into(ctxs, groups, self.kc, self.vc)  # [b, V]
+        self.check("prefill")
+        top, first = logp.to(self.score.dtype).topk(n, dim=-1)
+        idx = torch.tensor(groups, device=self.device)
+        rows = (idx[:, None] * n + torch.arange(n, device=self.device)).reshape(-1)
+        first = first.reshape(-1)
+        self.tok[rows] = first
+        self.score[rows] = top.reshape(-1)
+        self.ended[rows] = first == EOS
+        self.count[rows] = ((first != PAD) & (first != EOS)).long()
+        self.hist[rows, 0] = first.to(torch.int32)
+        lens = torch.tensor([c.size(0) for c in ctxs], device=self.device)
+        self.k_step[idx] = 1
+        self.ctx[idx] = lens
+        self.gdone[idx] = self.ended[rows].view(-1, n).all(-1) | (lens - 1 >= LIMIT)
 
-    def finish(self, finished: list[int]) -> None:
-        dec, n = self.dec, self.dec.beams
-        k_now = dec.k_step[: self.s].cpu().numpy()
-        hist = dec.hist[: self.s * n].cpu().numpy()
-        refill = []
-        for g in finished:
-            k = int(k_now[g])
-            tokens = [int(t) for t in hist[g * n, :k] if t not in (PAD, BOS, EOS)]
-            dec.stats["tokens"] += k
-            j = int(self.stream[g])
-            ctx = self.advance(j, tokens)
-            if ctx is None:
-                j = next(self.upcoming, None)
-                ctx = None if j is None else self.start(j)
-            self.stream[g] = -1
-            if ctx is not None:
-                refill.append((g, j, ctx))
-        if refill:
-            self.fill(refill)
+    def _best_tokens(self, sched: UnitScheduler, g: int) -> list[int]:
+        """Row 0 of a finished group: its tokens of this context (PAD / BOS / EOS dropped)."""
+        k = int(self.k_step[g])
+        self.stats["tokens"] += k
+        return [int(t) for t in self.hist[g * self.beams, :k].tolist() if t not in (PAD, BOS, EOS)]
 
-    def due_step(self, k0: int, c: int) -> int:
-        """First k >= k0 at which hist[k] sits at a checked position: c - 1 + k a multiple of ``CHECK_EVERY`` and
-        past c + ``CHECK_WINDOW`` (k >= ``CHECK_WINDOW`` + 2)."""
-        k = max(k0, CHECK_WINDOW + 2)
-        return k + (-(c - 1 + k)) % CHECK_EVERY
+    def _run_block(self, sched: UnitScheduler) -> None:
+        """Replay steps up to the next due repetition check of an active group (at most ``sync_every``), so that the
+        check applies exactly at its step, as in the reference; then run the checks that are due."""
+        s = sched.units
+        active = sched.active()
+        k_now = self.k_step[:s].cpu().numpy()
+        due = {g: next_check(int(k_now[g]), sched.assigned[g].ctx_len) for g in active}
+        steps = max(1, min(self.sync_every, min(due[g] - int(k_now[g]) + 1 for g in active)))
+        need = max(int(k_now[g]) for g in active) + steps + 1
+        if need + 1 > self.gcap:
+            self.ensure_beam(self.ccap, need + self.reserve)
+        ckeys = min(self.ccap, bucket(max(sched.assigned[g].ctx_len for g in active)))
+        run = self.beam_runner(s, ckeys)
+        self.check("runner")
+        for _ in range(steps):
+            run()
+            self.check("step")
+        self.stats["steps"] += steps
+        self.stats["rows_steps"] += steps * self.beams * len(active)
+        k_after = self.k_step[:s].cpu().numpy()
+        checks = [g for g in active if int(k_after[g]) - 1 == due[g]]
+        if checks:
+            self._repetition_stop(checks, due, s)
 
-    def run(self) -> None:
-        dec, s, n = self.dec, self.s, self.dec.beams
-        dec.gdone[:s] = True
-        dec.k_step[:s] = 1
-        dec.tok[: s * n] = 0
-        self.fill([(g, j, self.start(j)) for g, j in zip(range(s), self.upcoming)])
-        while True:
-            gdone = dec.gdone[:s].cpu().numpy()
-            finished = [g for g in range(s) if self.stream[g] >= 0 and gdone[g]]
-            if finished:
-                self.finish(finished)
-                continue
-            active = [g for g in range(s) if self.stream[g] >= 0]
-            if not active:
-                break
-            k_now = dec.k_step[:s].cpu().numpy()
-            # Run up to the step that chooses the token at the next checked position of an active group, so the
-            # repetition stop applies exactly there, as in the reference.
-            due = {g: self.due_step(int(k_now[g]), int(self.ctx_len[g])) for g in active}
-            steps = max(1, min(dec.sync_every, min(due[g] - int(k_now[g]) + 1 for g in active)))
-            need = max(int(k_now[g]) for g in active) + steps + 1
-            if need + 1 > dec.gcap:
-                dec.ensure_beam(dec.ccap, need + dec.reserve)
-            ckeys = min(dec.ccap, bucket(max(int(self.ctx_len[g]) for g in active)))
-            run = dec.beam_runner(s, ckeys)
-            dec.check("runner")
-            for _ in range(steps):
-                run()
-                dec.check("step")
-            dec.stats["steps"] += steps
-            dec.stats["rows_steps"] += steps * n * len(active)
-            k_after = dec.k_step[:s].cpu().numpy()
-            checks = [g for g in active if int(k_after[g]) - 1 == due[g]]
-            if checks:
-                self.repetition_check(checks, due)
-        if self.normal is not None and (dec.ccap, dec.gcap) != self.normal:
-            dec.release()
-
-    def repetition_check(self, checks: list[int], due: dict) -> None:
-        dec, n = self.dec, self.dec.beams
-        hist = dec.hist[: self.s * n].cpu().numpy()
+    def _repetition_stop(self, checks: list[int], due: dict, s: int) -> None:
+        """End the rows of ``checks`` whose last ``CHECK_WINDOW`` tokens before their due step compress more than
+        ``CHECK_RATIO``; a group whose rows have all ended is done."""
+        n = self.beams
+        hist = self.hist[: s * n].cpu().numpy()
         stop = [g * n + b for g in checks for b in range(n)
                 if compression_ratio(hist[g * n + b, due[g] - CHECK_WINDOW: due[g]]) > CHECK_RATIO]
-        if stop:
-            dec.stats["repetition_stops"] += len(stop)
-            dec.ended[torch.tensor(stop, device=dec.device)] = True
-            groups = torch.tensor(checks, device=dec.device)
-            dec.gdone[groups] |= dec.ended[: self.s * n].view(self.s, n)[groups].all(-1)
+        if not stop:
+            return
+        self.stats["repetition_stops"] += len(stop)
+        self.ended[torch.tensor(stop, device=self.device)] = True
+        groups = torch.tensor(checks, device=self.device)
+        self.gdone[groups] |= self.ended[: s * n].view(s, n)[groups].all(-1)
+
+    def _retire(self) -> None:
+        if self._normal_caps is not None and (self.ccap, self.gcap) != self._normal_caps:
+            self.release()
 
 
-__all__ = ["BeamDecoder", "bucket"]
+__all__ = ["BeamDecoder", "bucket", "next_check"]

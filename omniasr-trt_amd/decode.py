@@ -1,16 +1,18 @@
-"""Batched greedy decoding of the omniASR LLM decoder on MI355X: static KV cache, HIP graphs, host loop.
+"""Batched greedy decoding of the omniASR LLM decoder on MI355X: static KV cache, HIP-graph steps, continuous
+batching.
 
-Behaviour of the reference's ``GreedyDecoder`` (src/omniasr_trt/decode.py): each slot (row) keeps its own
-position; contexts of different lengths are prefilled together; a step writes each running row's K/V at its
-own position and attends to its own keys only (finished rows read none); one step -- layers, LM head, argmax,
-update -- is one HIP graph per (rows, key bucket), replayed ``sync_every`` times between two looks of the host
-(EOS, the length cap, the zlib repetition stop, refilling finished slots with the next context).
+Behaviour of the reference's ``GreedyDecoder`` (src/omniasr_trt/decode.py): every slot (row of the batch) decodes
+its own context at its own position; contexts of different lengths are prefilled together; a step feeds each
+running slot's newest token, appends its K/V at the slot's position and attends to that slot's keys only (a finished
+slot reads none); the host looks every ``sync_every`` steps -- EOS, the position cap, the zlib repetition stop, and a
+new context for each slot whose context ended.
 
-State per slot: ``out[r, t]`` is the token predicted from input position t; ``last[r]`` is the position of the
-newest token ``tok[r]``, which the next step feeds at ``last + 1``; ``done[r]`` marks a finished row.
+Slot state on the device, as the reference keeps it: ``out[r, t]`` is the token predicted from input position t,
+``last[r]`` the position of the newest token ``tok[r]`` (the next step feeds it at ``last + 1``), ``done[r]`` marks a
+finished slot.
 
-The device work of a step is the HIP kernels of ``kernels`` (RoPE + KV append, verify attention, argmax +
-acceptance) between the decoder's GEMMs; there is no PyTorch attention or update path.
+A step is the HIP kernels of ``kernels`` (RoPE + KV append, verify attention, argmax + acceptance) between the
+decoder's GEMMs, one HIP graph per (slots, key bucket).  There is no PyTorch attention or update path in the step.
 """
 
 from __future__ import annotations
@@ -22,114 +24,126 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 from torch import Tensor
+from torch.nn.utils.rnn import pad_sequence
 
 from . import kernels
+from .batching import GraphCache, UnitScheduler, packed_weights
 from .llm import BOS, EOS, MAX_GEN, PAD, early_stop_index
 from .modeling import DecoderModel
 
 KEY_BUCKET = 256
-LIMIT = MAX_GEN - 4  # the reference stops after generating from this position
-# The caches start this large so that contexts after a stream's first segment (two segments of audio, the
-# previous text, markers) do not grow them -- and the graphs captured on them -- in every call.
+LIMIT = MAX_GEN - 4  # the last input position the reference generates from
+# Initial cache length.  A streaming context after an input's first segment holds two segments of audio frames, the
+# previous segment's text and a few markers; starting at this size keeps those contexts from growing the caches (and
+# re-capturing the graphs) call after call.
 CONTEXT_FLOOR = 2048
 
 
-def fuse_projections(model: DecoderModel) -> list[tuple[Tensor, Tensor, Tensor, Tensor]]:
-    """Per layer (qkv [3D, D], output [D, D], gate|inner [2F, D], ffn output [D, F]): q/k/v and gate/inner
-    concatenated once into one GEMM operand each, the modules re-pointed at slices of them (no weight held
-    twice)."""
-    fused = []
-    for layer in model.llama_decoder.layers:
-        a, f = layer.self_attn, layer.ffn
-        if not hasattr(layer, "_qkv"):
-            with torch.no_grad():
-                qkv = torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight])
-                gi = torch.cat([f.gate_proj.weight, f.inner_proj.weight])
-            d, n = a.q_proj.weight.size(0), f.gate_proj.weight.size(0)
-            for j, p in enumerate((a.q_proj, a.k_proj, a.v_proj)):
-                p.weight = torch.nn.Parameter(qkv[j * d: (j + 1) * d], requires_grad=False)
-            f.gate_proj.weight = torch.nn.Parameter(gi[:n], requires_grad=False)
-            f.inner_proj.weight = torch.nn.Parameter(gi[n:], requires_grad=False)
-            layer._qkv, layer._gi = qkv, gi
-        fused.append((layer._qkv, a.output_proj.weight, layer._gi, f.output_proj.weight))
-    return fused
+def bucketed(n: int, bucket: int = KEY_BUCKET) -> int:
+    """``n`` rounded up to a multiple of ``bucket``."""
+    return -(-int(n) // bucket) * bucket
+
+
+def fuse_projections(model: DecoderModel):
+    """Per layer the four GEMM operands (q|k|v, attention output, gate|inner, FFN output) -- see
+    :func:`batching.packed_weights`.  (src/omniasr_trt/decode.py:34-54)"""
+    return packed_weights(model)
+
+
+def _regrown(old: Tensor | None, shape: tuple, dim: int, fill, dtype, device) -> Tensor:
+    """A new tensor of ``shape`` filled with ``fill`` that starts with ``old``'s contents along ``dim``."""
+    new = torch.full(shape, fill, dtype=dtype, device=device)
+    if old is not None:
+        new.narrow(dim, 0, old.size(dim)).copy_(old)
+    return new
 
 
 class GreedyDecoder:
+    """Greedy search with up to ``max_batch`` contexts in flight (the reference's constructor arguments)."""
+
     def __init__(self, model: DecoderModel, *, max_batch: int = 16, sync_every: int = 16, graphs: bool = True,
                  reserve: int = 768, fused: bool = True):
-        self.m = model
-        cfg = model.dec_cfg
-        self.dtype = model.final_proj.weight.dtype
-        self.device = model.final_proj.weight.device
         if not fused:
             raise ValueError("this build has one decode path, the HIP kernels (fused=False is not available)")
+        self.m = model
+        self.dtype = model.final_proj.weight.dtype
+        self.device = model.final_proj.weight.device
         if not kernels.available(self.device):
             raise RuntimeError(f"the decoder runs on the MI355X kernels: {self.device} is not a GPU device")
+        cfg = model.dec_cfg
         self.fused = True
         self.layers = fuse_projections(model)
         self.heads = cfg.num_heads
         self.head_dim = cfg.model_dim // cfg.num_heads
         self.max_batch = max_batch
         self.sync_every = sync_every
-        self.step_tokens = 1  # positions a row advances by at most in one step
-        self.use_graphs = graphs
-        self.debug_sync = os.environ.get("OMNIASR_TRT_DEBUG_SYNC") == "1"  # synchronise after each operation
-        if self.use_graphs:
-            self.pool = torch.cuda.graph_pool_handle()
-            self.capture_stream = torch.cuda.Stream(self.device)
-        self.reserve = reserve  # generated positions beyond the longest context before the cache grows
+        self.step_tokens = 1  # positions a slot can advance by in one step
+        self.reserve = reserve  # positions beyond the longest context allocated up front
         self.context_floor = CONTEXT_FLOOR
+        self.use_graphs = graphs
+        self.graphs = GraphCache(self.device, graphs)
+        self.debug_sync = os.environ.get("OMNIASR_TRT_DEBUG_SYNC") == "1"  # synchronise after each operation
+        self.phase = lambda name: nullcontext()  # the transcriber's timer when profiling
+        self.stats = {"steps": 0, "rows_steps": 0, "tokens": 0, "prefill_tokens": 0, "captures": 0, "grows": 0}
         self.capacity = 0
         self.k = self.v = self.out = None
-        self.graphs: dict = {}
-        self.stats = {"steps": 0, "rows_steps": 0, "tokens": 0, "prefill_tokens": 0, "captures": 0, "grows": 0}
-        b, dev = max_batch, self.device
-        self.tok = torch.zeros(b, device=dev, dtype=torch.long)
-        self.last = torch.zeros(b, device=dev, dtype=torch.long)
-        self.done = torch.ones(b, device=dev, dtype=torch.bool)
-        self.phase = lambda name: nullcontext()  # the transcriber's timer when profiling
+        self._normal_capacity: int | None = None
+        self._host: tuple | None = None  # (out, last) read back at the current look
+        rows, dev = max_batch, self.device
+        self.tok = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.last = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.done = torch.ones(rows, dtype=torch.bool, device=dev)
 
     # ------------------------------------------------------------------ persistent buffers
 
     def ensure_capacity(self, length: int) -> None:
-        """KV cache and token buffer for ``length`` positions (graphs hold their addresses, so they persist)."""
-        length = min(-(-length // KEY_BUCKET) * KEY_BUCKET, -(-MAX_GEN // KEY_BUCKET) * KEY_BUCKET)
-        if length <= self.capacity:
+        """Make the KV cache and the token buffer hold ``length`` positions (rounded up to the key bucket, at most the
+        position cap).  Growing keeps the contents and drops the graphs, which hold the old addresses."""
+        target = min(bucketed(length), bucketed(MAX_GEN))
+        if target <= self.capacity:
             return
-        b, dev = self.max_batch, self.device
-        torch.cuda.synchronize(dev)  # no step in flight while buffers and graphs are replaced
-        shape = (len(self.layers), b, self.heads, length, self.head_dim)
-        k = torch.zeros(shape, device=dev, dtype=self.dtype)
-        v = torch.zeros(shape, device=dev, dtype=self.dtype)
-        out = torch.full((b, length), PAD, device=dev, dtype=torch.int32)
+        torch.cuda.synchronize(self.device)  # nothing in flight on the buffers being replaced
+        kv_shape = (len(self.layers), self.max_batch, self.heads, target, self.head_dim)
+        self.k = _regrown(self.k, kv_shape, 3, 0, self.dtype, self.device)
+        self.v = _regrown(self.v, kv_shape, 3, 0, self.dtype, self.device)
+        self.out = _regrown(self.out, (self.max_batch, target), 1, PAD, torch.int32, self.device)
         if self.capacity:
-            k[..., : self.capacity, :] = self.k
-            v[..., : self.capacity, :] = self.v
-            out[:, : self.capacity] = self.out
             self.stats["grows"] += 1
-        self.k, self.v, self.out, self.capacity = k, v, out, length
-        self.reset_graphs()  # captured against the old buffers
-
-    def check(self, where: str) -> None:
-        if self.debug_sync:
-            try:
-                torch.cuda.synchronize(self.device)
-            except Exception as e:
-                raise RuntimeError(f"GPU error after {where} (capacity {self.capacity})") from e
+        self.capacity = target
+        self.reset_graphs()
 
     def reset_graphs(self) -> None:
-        """Drop the captured graphs and start a new memory pool."""
         self.graphs.clear()
-        if self.use_graphs:
-            self.pool = torch.cuda.graph_pool_handle()
 
     def release(self) -> None:
-        """Drop the KV cache and the graphs captured on it (the next call allocates its normal size again)."""
+        """Free the KV cache and the graphs captured on it; the next call allocates its normal size again."""
         torch.cuda.synchronize(self.device)
         self.k = self.v = self.out = None
         self.capacity = 0
         self.reset_graphs()
+
+    def check(self, where: str) -> None:
+        if not self.debug_sync:
+            return
+        try:
+            torch.cuda.synchronize(self.device)
+        except Exception as e:
+            raise RuntimeError(f"GPU error after {where} (capacity {self.capacity})") from e
+
+    # ------------------------------------------------------------------ the decoder layers
+
+    def _layer(self, i: int, h: Tensor, attend) -> None:
+        """Decoder layer ``i`` on the residual stream ``h`` [N, D] in place; ``attend(qkv)`` returns the attention
+        output [N, H*Dh] for the layer's q|k|v [N, 3*H*Dh] (it also writes the K/V cache)."""
+        w = self.layers[i]
+        layer = self.m.llama_decoder.layers[i]
+        o = attend(layer.self_attn_layer_norm(h) @ w.qkv.t())
+        h.addmm_(o, w.attn_out.t())  # the GEMM adds into the residual in place
+        gate, inner = (layer.ffn_layer_norm(h) @ w.gate_inner.t()).chunk(2, -1)
+        h.addmm_(inner * F.silu(gate), w.ffn_out.t())
+
+    def _head(self, h: Tensor) -> Tensor:
+        return self.m.final_proj(self.m.llama_decoder.layer_norm(h))
 
     # ------------------------------------------------------------------ prefill
 
@@ -138,242 +152,196 @@ class GreedyDecoder:
         return self.prefill_into(ctx, slots, self.k, self.v).argmax(-1)
 
     def prefill_into(self, ctx: list[Tensor], slots, k_cache: Tensor, v_cache: Tensor) -> Tensor:
-        """Contexts into rows ``slots`` of ``k_cache`` / ``v_cache`` ([layers, rows, H, S, Dh]) -- RoPE and the cache
-        writes by ``kernels.rope_kv``, causal attention over each context by ``kernels.prefill_attention`` (bf16, head
-        dim 128, 256 or 512; fp32 torch attention otherwise); returns the log-softmax after each context's last token [B, V]
-        (model dtype).  (src/omniasr_trt/decode.py:137-179)"""
-        m, b = self.m, len(ctx)
-        lens = [c.size(0) for c in ctx]
-        width = max(lens)
-        rows = None if slots is None or list(slots) == list(range(b)) else torch.tensor(slots, device=self.device)
-        x = torch.zeros(b, width, ctx[0].size(1), device=self.device, dtype=self.dtype)
-        for j, c in enumerate(ctx):
-            x[j, : lens[j]] = c
-        h = x.view(b * width, -1)
+        """The contexts (right-padded to the longest) through the decoder into rows ``slots`` of ``k_cache`` /
+        ``v_cache`` ([layers, rows, H, S, Dh]); returns the log-softmax after each context's last token [B, V] in the
+        model's dtype.  RoPE and the cache writes are ``kernels.rope_kv``; causal attention over each context is
+        ``kernels.prefill_attention`` (bf16, head dim 128 / 256 / 512) or fp32 torch attention otherwise.  Padding
+        comes after each context's tokens, and attention is causal, so no context position sees a pad.
+        (src/omniasr_trt/decode.py:137-179)"""
+        b = len(ctx)
+        lens = torch.tensor([c.size(0) for c in ctx], device=self.device)
+        width = int(lens.max())
+        rows = torch.arange(b, device=self.device) if slots is None else torch.as_tensor(list(slots),
+                                                                                           device=self.device)
+        h = pad_sequence([c.to(self.dtype) for c in ctx], batch_first=True).reshape(b * width, -1).contiguous()
         pos = torch.arange(width, device=self.device).repeat(b)
-        ctx_rows = torch.arange(b, device=self.device) if rows is None else rows
-        slot = ctx_rows.repeat_interleave(width)
-        fused = kernels.prefill_supported(self.dtype, self.head_dim)
-        for i, layer in enumerate(m.llama_decoder.layers):
-            qkv_w, out_w, gi_w, ffo_w = self.layers[i]
-            qkv = layer.self_attn_layer_norm(h) @ qkv_w.t()
-            q = kernels.rope_kv(qkv, m.rope, pos, k_cache[i], v_cache[i], self.heads, slot)
-            # Right padding and causal attention: no valid token sees a pad.
-            if fused:  # bf16, head dim 128 / 256 / 512: the HIP causal attention over the cache rows just written
-                o = kernels.prefill_attention(q, k_cache[i], v_cache[i], ctx_rows, width, self.head_dim ** -0.5)
-                o = o.view(b * width, -1)
-            else:  # fp32 math keeps bf16 batched products (and their transposed operands) out of this path
-                q = q.view(b, width, self.heads, -1).transpose(1, 2)
-                k = k_cache[i, :b, :, :width] if rows is None else k_cache[i, rows, :, :width]
-                v = v_cache[i, :b, :, :width] if rows is None else v_cache[i, rows, :, :width]
-                o = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True).to(self.dtype)
-                o = o.transpose(1, 2).reshape(b * width, -1)
-            h.addmm_(o, out_w.t())  # in place: the GEMM adds into the residual, no copy of it
-            gate, inner = (layer.ffn_layer_norm(h) @ gi_w.t()).chunk(2, -1)
-            h.addmm_(inner * F.silu(gate), ffo_w.t())
-        h = h.view(b, width, -1)
-        last = h[torch.arange(b, device=self.device), torch.tensor(lens, device=self.device) - 1]
-        logits = m.final_proj(m.llama_decoder.layer_norm(last))
-        self.stats["prefill_tokens"] += sum(lens)
-        return F.log_softmax(logits, dim=-1)
+        row_of = rows.repeat_interleave(width)
+        scale = self.head_dim ** -0.5
+        on_kernel = kernels.prefill_supported(self.dtype, self.head_dim)
+        for i in range(len(self.layers)):
+            kc, vc = k_cache[i], v_cache[i]
+
+            def attend(qkv, kc=kc, vc=vc):
+                q = kernels.rope_kv(qkv, self.m.rope, pos, kc, vc, self.heads, row_of)
+                if on_kernel:
+                    return kernels.prefill_attention(q, kc, vc, rows, width, scale).view(b * width, -1)
+                # fp32 models and other head dims: torch attention in fp32 over the rows just written (fp32 keeps
+                # bf16 batched products, and their transposed operands, out of this path)
+                qf = q.view(b, width, self.heads, -1).transpose(1, 2).float()
+                kf = kc[rows, :, :width].float()
+                vf = vc[rows, :, :width].float()
+                o = F.scaled_dot_product_attention(qf, kf, vf, is_causal=True).to(self.dtype)
+                return o.transpose(1, 2).reshape(b * width, -1)
+
+            self._layer(i, h, attend)
+        final = h.view(b, width, -1)[torch.arange(b, device=self.device), lens - 1]
+        self.stats["prefill_tokens"] += int(lens.sum())
+        return F.log_softmax(self._head(final), dim=-1)
 
     # ------------------------------------------------------------------ one decode step
 
     def layer_stack(self, h: Tensor, pos: Tensor, slots: Tensor | None, lengths: Tensor, tokens: int,
                     keys: int) -> Tensor:
-        """The decoder layers over the fed tokens ``h`` [B*T, D]; returns the LM-head logits [B*T, V]."""
-        m = self.m
+        """The decoder layers over the fed tokens ``h`` [B*T, D] (T = ``tokens`` per slot, at ``pos``, written to
+        cache rows ``slots``, each slot's queries over its ``lengths`` keys plus the causal new ones); returns the
+        LM-head logits [B*T, V]."""
         scale = self.head_dim ** -0.5
-        rows = h.size(0)
-        for i, layer in enumerate(m.llama_decoder.layers):
-            qkv_w, out_w, gi_w, ffo_w = self.layers[i]
-            qkv = layer.self_attn_layer_norm(h) @ qkv_w.t()
-            q = kernels.rope_kv(qkv, m.rope, pos, self.k[i], self.v[i], self.heads, slots)
-            o = kernels.draft_attention(q, self.k[i], self.v[i], lengths, tokens, keys, scale).reshape(rows, -1)
-            h.addmm_(o, out_w.t())  # in place: the GEMM adds into the residual, no copy of it
-            gate, inner = (layer.ffn_layer_norm(h) @ gi_w.t()).chunk(2, -1)
-            h.addmm_(inner * F.silu(gate), ffo_w.t())
-        return m.final_proj(m.llama_decoder.layer_norm(h))
+        n = h.size(0)
+        for i in range(len(self.layers)):
+            kc, vc = self.k[i], self.v[i]
+
+            def attend(qkv, kc=kc, vc=vc):
+                q = kernels.rope_kv(qkv, self.m.rope, pos, kc, vc, self.heads, slots)
+                return kernels.draft_attention(q, kc, vc, lengths, tokens, keys, scale).reshape(n, -1)
+
+            self._layer(i, h, attend)
+        return self._head(h)
 
     def step(self, b: int, keys: int) -> None:
-        """In place on rows 0..b-1 of the persistent buffers; finished rows are left as they are.
-        (src/omniasr_trt/decode.py:183-224)"""
+        """One token for every running slot 0..b-1, in place; finished slots keep their state (they are fed again at
+        their last position, read no keys, and nothing they produce is kept).  (src/omniasr_trt/decode.py:183-224)"""
         tok, last, done, out = self.tok[:b], self.last[:b], self.done[:b], self.out[:b]
         running = ~done
-        p = last + running.long()  # input position of ``tok``; finished rows recompute their last slot
-        lengths = torch.where(running, p + 1, 0)  # finished rows read no keys (their outputs are not kept)
-        h = self.m.text_frontend.weight[tok]  # [B, D]
-        logits = self.layer_stack(h, p, None, lengths, 1, keys)
+        p = last + running.long()
+        lengths = torch.where(running, p + 1, 0)
+        logits = self.layer_stack(self.m.text_frontend.weight[tok], p, None, lengths, 1, keys)
         kernels.greedy_accept(logits, tok[:, None], out, tok, last, done, None, None, None, LIMIT, EOS)
 
     def state(self) -> list[Tensor]:
-        """The per-slot buffers a step changes (restored after the warm-up step of a capture)."""
+        """The per-slot buffers a step changes besides the caches."""
         return [self.tok, self.last, self.done, self.out]
 
     def filled(self, slots: list[int], streams: list[int]) -> None:
-        """Called after ``slots`` were prefilled with a context of ``streams`` (subclasses add their state)."""
+        """Hook called after ``slots`` were given a context of ``streams`` (the drafted decoder loads drafts)."""
 
     def runner(self, b: int, keys: int):
-        """The step on rows 0..b-1 with ``keys`` cache positions in reach: a replayed HIP graph per (b, keys)."""
-        if not self.use_graphs:
-            return lambda: self.step(b, keys)
-        key = (b, keys)
-        if key not in self.graphs:
-            # Captured by hand on a side stream into one shared pool; a warm-up step outside the capture first
-            # (it also allocates what the kernels keep between calls), then the state it changed is restored
-            # (the K/V it wrote are rewritten identically by the replay).
-            torch.cuda.synchronize(self.device)
-            saved = [t[:b].clone() for t in self.state()]
-            stream = self.capture_stream
-            stream.wait_stream(torch.cuda.current_stream(self.device))
-            with torch.cuda.stream(stream):
-                self.step(b, keys)
-                for t, v in zip(self.state(), saved, strict=True):
-                    t[:b].copy_(v)
-                graph = torch.cuda.CUDAGraph()
-                graph.capture_begin(pool=self.pool)
-                self.step(b, keys)
-                graph.capture_end()
-            torch.cuda.current_stream(self.device).wait_stream(stream)
-            torch.cuda.synchronize(self.device)
-            self.graphs[key] = graph
-            self.stats["captures"] += 1
-        return self.graphs[key].replay
+        """The step of slots 0..b-1 with ``keys`` positions in reach, as a callable: a graph replay per (b, keys)."""
+        before = self.graphs.captures
+        run = self.graphs.runner((b, keys), lambda: self.step(b, keys), lambda: [t[:b] for t in self.state()])
+        self.stats["captures"] += self.graphs.captures - before
+        return run
 
-    # ------------------------------------------------------------------ generate
+    # ------------------------------------------------------------------ streams
 
     @torch.inference_mode()
     def generate(self, contexts: list[Tensor]) -> list[list[int]]:
         """Greedy text tokens of each context (``[C, D]`` embeddings ending with <bos>)."""
-        results: list = [None] * len(contexts)
+        texts: list = [None] * len(contexts)
 
-        def finish(j, tokens):
-            results[j] = tokens
+        def keep(j, tokens):
+            texts[j] = tokens
             return None
 
-        self.decode_streams(len(contexts), contexts.__getitem__, finish)
-        return results
+        self.decode_streams(len(contexts), contexts.__getitem__, keep)
+        return texts
 
     @torch.inference_mode()
     def decode_streams(self, n: int, start, advance) -> None:
-        """Decode ``n`` independent streams of contexts with up to ``max_batch`` of them in flight.
+        """Decode ``n`` independent streams of contexts, up to ``max_batch`` at once.  ``start(j)`` gives stream j's
+        first context; ``advance(j, tokens)`` gets the greedy tokens of its current context and returns the next
+        context, or None when the stream is over.  (src/omniasr_trt/decode.py:274-373)"""
+        b = min(self.max_batch, n)
+        # Idle slots run in the step graph too (reading no keys, writing at ``last``): park them at position 0, as a
+        # previous call may have left positions past a cache released since.
+        self.done[:b] = True
+        self.last[:b] = 0
+        self.tok[:b] = 0
+        self._normal_capacity = None
+        UnitScheduler(b, n, start, advance, admit=self._admit, finished=lambda: self._finished(b),
+                      harvest=self._harvest, run_block=self._run_block, retire=self._retire).run()
 
-        ``start(j)`` gives stream j's first context; ``advance(j, tokens)`` receives the greedy tokens of its current
-        context and returns its next one (None: the stream is finished).  A slot whose context is finished takes its
-        stream's next context (or a new stream) at the next host look, so the batch stays full.
-        (src/omniasr_trt/decode.py:274-373)"""
-        slots = _Slots(self, min(self.max_batch, n), iter(range(n)), start, advance)
-        slots.run()
+    def _host_state(self, b: int) -> tuple[np.ndarray, np.ndarray]:
+        """``out`` and ``last`` of slots 0..b-1 on the host, read once per look."""
+        if self._host is None:
+            self._host = (self.out[:b].cpu().numpy(), self.last[:b].cpu().numpy())
+        return self._host
 
+    def _finished(self, b: int) -> list[int]:
+        self._host = None  # a new look
+        return np.flatnonzero(self.done[:b].cpu().numpy()).tolist()
 
-class _Slots:
-    """Host side of ``decode_streams``: which stream each slot decodes and what the host has checked of it."""
+    def _admit(self, sched: UnitScheduler, pairs: list) -> None:
+        """Prefill the contexts into their slots and start them: the prefill's argmax is the first token, predicted
+        from the context's last position."""
+        slots = [u for u, _, _ in pairs]
+        ctxs = [c for _, _, c in pairs]
+        others = [u for u in sched.active() if u not in set(slots)]
+        want = max(max(c.size(0) for c in ctxs), self.context_floor) + self.reserve
+        if others:  # slots still decoding must keep room for a whole block of steps
+            lasts = self.last[torch.tensor(others, device=self.device)]
+            want = max(want, int(lasts.max()) + self.sync_every * self.step_tokens + 2)
+        self.ensure_capacity(want)
+        if self._normal_capacity is None:
+            self._normal_capacity = self.capacity
+        with self.phase("prefill"):
+            first = self.prefill(ctxs, slots)
+        self.check("prefill")
+        idx = torch.tensor(slots, device=self.device)
+        pos = torch.tensor([c.size(0) - 1 for c in ctxs], device=self.device)
+        self.out[idx] = PAD
+        self.out[idx, pos] = first.to(torch.int32)
+        self.tok[idx] = first
+        self.last[idx] = pos
+        self.done[idx] = (first == EOS) | (pos >= LIMIT)
+        self.filled(slots, [j for _, j, _ in pairs])
+        self._host = None
 
-    def __init__(self, dec: GreedyDecoder, b: int, upcoming, start, advance):
-        self.dec, self.b = dec, b
-        self.upcoming, self.start, self.advance = upcoming, start, advance
-        self.stream = np.full(b, -1)  # stream decoded in each slot (-1: idle)
-        self.ctx_len = np.zeros(b, dtype=np.int64)
-        self.checked = np.zeros(b, dtype=np.int64)  # positions up to which the repetition check has run
-        self.stopped = np.full(b, -1)  # position of a repetition stop
-        self.normal: int | None = None
+    def _harvest(self, sched: UnitScheduler, u: int) -> list[int]:
+        """The tokens of slot u's finished context: predicted from its last context position up to its last
+        position, or up to a repetition stop (that token kept); PAD / BOS / EOS dropped."""
+        a = sched.assigned[u]
+        out, last = self._host_state(sched.units)
+        end = a.stop if a.stop >= 0 else int(last[u])
+        self.stats["tokens"] += end - a.ctx_len + 2
+        return [int(t) for t in out[u, a.ctx_len - 1: end + 1] if t not in (PAD, BOS, EOS)]
 
-    def fill(self, pairs: list) -> None:
-        """Prefill ``pairs`` [(slot, stream, context)] and reset those slots."""
-        dec, b = self.dec, self.b
-        refilled = {s for s, _, _ in pairs}
-        in_flight = [int(dec.last[s]) for s in range(b) if self.stream[s] >= 0 and s not in refilled]
-        longest = max(c.size(0) for _, _, c in pairs)
-        dec.ensure_capacity(max([max(longest, dec.context_floor) + dec.reserve] +
-                                [p + dec.sync_every * dec.step_tokens + 2 for p in in_flight]))
-        self.normal = self.normal or dec.capacity
-        slots = [s for s, _, _ in pairs]
-        with dec.phase("prefill"):
-            first = dec.prefill([c for _, _, c in pairs], slots)
-        dec.check("prefill")
-        idx = torch.tensor(slots, device=dec.device)
-        pos = torch.tensor([c.size(0) - 1 for _, _, c in pairs], device=dec.device)
-        dec.out[idx] = PAD
-        dec.out[idx, pos] = first.to(torch.int32)
-        dec.tok[idx] = first
-        dec.last[idx] = pos
-        dec.done[idx] = (first == EOS) | (pos >= LIMIT)
-        for s, j, c in pairs:
-            self.stream[s], self.ctx_len[s], self.checked[s], self.stopped[s] = j, c.size(0), c.size(0) - 1, -1
-        dec.filled(slots, [j for _, j, _ in pairs])
-
-    def finish(self, finished: list[int]) -> None:
-        """Hand the tokens of finished slots to their streams and refill the slots."""
-        dec = self.dec
-        out = dec.out[: self.b].cpu().numpy()
-        last = dec.last[: self.b].cpu().numpy()
-        refill = []
-        for s in finished:
-            end = int(self.stopped[s]) if self.stopped[s] >= 0 else int(last[s])
-            tokens = [int(t) for t in out[s, self.ctx_len[s] - 1: end + 1] if t not in (PAD, BOS, EOS)]
-            dec.stats["tokens"] += end - int(self.ctx_len[s]) + 2
-            j = int(self.stream[s])
-            ctx = self.advance(j, tokens)
-            if ctx is None:
-                j = next(self.upcoming, None)
-                ctx = None if j is None else self.start(j)
-            self.stream[s] = -1
-            if ctx is not None:
-                refill.append((s, j, ctx))
-        if refill:
-            self.fill(refill)
-
-    def run(self) -> None:
-        dec, b = self.dec, self.b
-        # Idle slots still run in the step graph (reading no keys) and write at their ``last`` position: reset it, as
-        # a previous call may have left positions beyond a cache released since.
-        dec.done[:b] = True
-        dec.last[:b] = 0
-        dec.tok[:b] = 0
-        self.fill([(s, j, self.start(j)) for s, j in zip(range(b), self.upcoming)])
-        while True:
-            done = dec.done[:b].cpu().numpy()
-            finished = [s for s in range(b) if self.stream[s] >= 0 and done[s]]
-            if finished:
-                self.finish(finished)
-                continue  # a refilled slot may be finished at once (first token EOS)
-            active = self.stream >= 0
-            if not active.any():
-                break
-            last = dec.last[:b].cpu().numpy()
-            need = int(last[active].max()) + dec.sync_every * dec.step_tokens + 2
-            if need > dec.capacity:
-                dec.ensure_capacity(need + dec.reserve)
-                dec.check("grow")
-            keys = min(dec.capacity, -(-need // KEY_BUCKET) * KEY_BUCKET)
-            run = dec.runner(b, keys)
-            dec.check("runner")
-            for _ in range(dec.sync_every):
-                run()
-                dec.check("step")
-            dec.stats["steps"] += dec.sync_every
-            dec.stats["rows_steps"] += dec.sync_every * int((active & ~done).sum())
-            self.repetition_check()
-        if self.normal is not None and dec.capacity > self.normal:
-            # A long generation grew the cache; a long-lived process must not keep that, so the next call starts
-            # from its normal size again.
-            dec.release()
-
-    def repetition_check(self) -> None:
-        dec, b = self.dec, self.b
-        out = dec.out[:b].cpu().numpy()
-        last = dec.last[:b].cpu().numpy()
-        stop_now = []
-        for s in range(b):
-            if self.stream[s] < 0 or self.stopped[s] >= 0:
+    def _run_block(self, sched: UnitScheduler) -> None:
+        """``sync_every`` step replays on a key bucket that holds every active slot's keys after them, then the
+        repetition check of each active slot up to its new position."""
+        b = sched.units
+        active = sched.active()
+        _, last = self._host_state(b)
+        need = int(max(last[u] for u in active)) + self.sync_every * self.step_tokens + 2
+        if need > self.capacity:
+            self.ensure_capacity(need + self.reserve)
+            self.check("grow")
+        run = self.runner(b, min(self.capacity, bucketed(need)))
+        self.check("runner")
+        for _ in range(self.sync_every):
+            run()
+            self.check("step")
+        self.stats["steps"] += self.sync_every
+        self.stats["rows_steps"] += self.sync_every * len(active)  # every active slot was running at the look
+        self._host = None
+        out, last = self._host_state(b)
+        stopped = []
+        for u in active:
+            a = sched.assigned[u]
+            if a.stop >= 0:
                 continue
-            hit = early_stop_index(out[s], int(self.checked[s]) + 1, int(last[s]), int(self.ctx_len[s]))
-            self.checked[s] = last[s]
+            hit = early_stop_index(out[u], a.checked + 1, int(last[u]), a.ctx_len)
+            a.checked = int(last[u])
             if hit is not None:
-                self.stopped[s] = hit
-                stop_now.append(s)
-        if stop_now:
-            dec.done[torch.tensor(stop_now, device=dec.device)] = True
+                a.stop = hit
+                stopped.append(u)
+        if stopped:
+            self.done[torch.tensor(stopped, device=self.device)] = True
+
+    def _retire(self) -> None:
+        # A long generation may have grown the cache (up to the position cap for every slot); a long-lived process
+        # does not keep that: the next call starts from its normal size again.
+        if self._normal_capacity is not None and self.capacity > self._normal_capacity:
+            self.release()
 
 
-__all__ = ["CONTEXT_FLOOR", "GreedyDecoder", "KEY_BUCKET", "LIMIT", "fuse_projections"]
+__all__ = ["CONTEXT_FLOOR", "GreedyDecoder", "KEY_BUCKET", "LIMIT", "bucketed", "fuse_projections"]

@@ -24,12 +24,15 @@ from .decode import LIMIT, GreedyDecoder  # LIMIT: this module's, read at call t
 from .llm import EOS
 from .modeling import DecoderModel
 
-DRAFT_CAPACITY = 1024  # draft tokens kept per row (a 15 s segment's CTC text is rarely longer than 400)
-NGRAM = 8  # newest tokens matched against the draft / the row's own tokens
-BEHIND, AHEAD = 64, 160  # draft positions searched before / after the expected one
-# Matching tokens a draft position needs at each distance from the expected one (<= 1, <= 4, <= 12, <= 40, beyond).
+# The proposal's search constants (src/omniasr_trt/spec.py:35-40); they decide which tokens are proposed, so they
+# are the reference's values.
+DRAFT_CAPACITY = 1024  # draft ids held per slot; longer drafts are cut (a 15 s CTC transcript is far shorter)
+NGRAM = 8  # how many of a slot's newest tokens a candidate position is matched against
+BEHIND, AHEAD = 64, 160  # the draft window around the expected draft position: positions before / after it
+# (distance, matches): a draft position at most ``distance`` from the expected one needs ``matches`` leading matches;
+# farther positions need NGRAM.  The search cannot jump to a common token far away on a short match.
 REACH = ((1, 1), (4, 2), (12, 4), (40, 6))
-SELF_WINDOW, SELF_MIN = 256, 3  # own positions searched back, matching tokens needed
+SELF_WINDOW, SELF_MIN = 256, 3  # own-token search: how far back it looks, and the matches it needs to be used
 
 
 class SpecDecoder(GreedyDecoder):
@@ -41,32 +44,37 @@ class SpecDecoder(GreedyDecoder):
         self.draft_tokens = draft_tokens
         self.step_tokens = draft_tokens + 1
         self.ngram, self.self_min = ngram, self_min
-        b, dev = max_batch, self.device
-        self.draft = torch.full((b, DRAFT_CAPACITY), -1, device=dev, dtype=torch.int32)
-        self.draft_len = torch.zeros(b, device=dev, dtype=torch.long)
-        self.next = torch.zeros(b, device=dev, dtype=torch.long)  # draft position expected after ``tok``
-        self.first = torch.zeros(b, device=dev, dtype=torch.long)  # position of the segment's first token
-        self.start = torch.zeros(b, device=dev, dtype=torch.long)  # draft position of a step's first proposal
-        # The transcriber's: a stream's draft for its current context, (token ids, draft position of the first
-        # generated token), or None.
+        rows, dev = max_batch, self.device
+        # Per-slot drafting state, in the layouts the proposal kernel reads: the draft ids (-1 padded) and their
+        # count; ``next``, the draft position the search expects to hold the successor of ``tok``; ``first``, the
+        # lower bound of the own-token search (the context's last position); ``start``, written by every step, the
+        # draft position its proposal was taken from.
+        self.draft = torch.full((rows, DRAFT_CAPACITY), -1, device=dev, dtype=torch.int32)
+        self.draft_len = torch.zeros(rows, device=dev, dtype=torch.long)
+        self.next = torch.zeros(rows, device=dev, dtype=torch.long)
+        self.first = torch.zeros(rows, device=dev, dtype=torch.long)
+        self.start = torch.zeros(rows, device=dev, dtype=torch.long)
+        # Set by the transcriber: stream j -> None or (draft ids, draft position of the context's first generated
+        # token) for the stream's current context.
         self.drafts = lambda stream: None
 
     def state(self) -> list[Tensor]:
         return super().state() + [self.next]
 
     def filled(self, slots: list[int], streams: list[int]) -> None:
-        """Load each refilled slot's draft (one host-to-device copy per slot fill, not per step).
+        """Load the draft of each newly filled slot's stream (one host-to-device copy per context, none per step).
+        ``drafts(j)`` is None or (ids, where): ``where`` is the draft position of the context's first generated token,
+        so the proposal search starts just after it; the own-token search starts at the context's last position.
         (src/omniasr_trt/spec.py:64-74)"""
-        for s, j in zip(slots, streams, strict=True):
-            draft = self.drafts(j)
-            tokens, start = draft if draft is not None else ([], 0)
-            tokens = list(tokens)[:DRAFT_CAPACITY]
-            self.draft[s] = -1
-            if tokens:
-                self.draft[s, : len(tokens)] = torch.as_tensor(tokens, dtype=torch.int32).to(self.device)
-            self.draft_len[s] = len(tokens)
-            self.next[s] = start + 1
-            self.first[s] = self.last[s]
+        for slot, stream in zip(slots, streams, strict=True):
+            given = self.drafts(stream)
+            ids, where = ([], 0) if given is None else (list(given[0])[:DRAFT_CAPACITY], int(given[1]))
+            row = torch.full((DRAFT_CAPACITY,), -1, dtype=torch.int32)
+            row[: len(ids)] = torch.as_tensor(ids, dtype=torch.int32)
+            self.draft[slot].copy_(row)
+            self.draft_len[slot] = len(ids)
+            self.next[slot] = where + 1
+            self.first[slot] = self.last[slot]
 
     def propose(self, b: int) -> tuple[Tensor, Tensor]:
         """Per row the next ``draft_tokens`` proposed tokens [B, k] and whether they came from the draft [B].

@@ -95,8 +95,13 @@ class Fp64Decoder:
 
 
 @torch.inference_mode()
-def greedy_reference(dec: Fp64Decoder, ctx: torch.Tensor, limit: int = MAX_GEN - 4) -> list[int]:
-    """Greedy tokens of one context [C, D] (ending with <bos>), in the reference's order of computation."""
+def greedy_reference(dec: Fp64Decoder, ctx: torch.Tensor, limit: int = MAX_GEN - 4,
+                     margins: list | None = None) -> list[int]:
+    """Greedy tokens of one context [C, D] (ending with <bos>), in the reference's order of computation.
+
+    ``margins``: if a list, receives per step the gap between the largest and the second largest log-probability
+    (float64): where it is below the error of another arithmetic (bf16 activations, another summation order), that
+    arithmetic may pick the other token, and both are correct roundings of the same search."""
     ctx = ctx.detach().to("cpu", torch.float64)
     c = ctx.size(0)
     cache = [None] * dec.layers
@@ -107,7 +112,11 @@ def greedy_reference(dec: Fp64Decoder, ctx: torch.Tensor, limit: int = MAX_GEN -
     t = c - 1
     while True:
         h = dec.forward(x[None], torch.tensor([t]), cache)
-        token = int(F.log_softmax(dec.logits(h[0]), -1).argmax())
+        logp = F.log_softmax(dec.logits(h[0]), -1)
+        token = int(logp.argmax())
+        if margins is not None:
+            top2 = torch.topk(logp, 2).values
+            margins.append(float(top2[0] - top2[1]))
         out[t] = token
         done = token == EOS
         if t % CHECK_EVERY == 0 and t > c + CHECK_WINDOW:
