@@ -25,6 +25,7 @@ import json
 import math
 import os
 import platform
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -100,8 +101,10 @@ class Workload:
         dec.done[:b] = False
         dec.draft_len[:b] = 0  # own tokens only (no CTC drafter)
         dec.next[:b] = 1
+        self.pkg = pkg
+        self.first_history = dec.first[:b].clone()
         self.snapshot = {k: getattr(dec, k)[:b].clone() for k in ("tok", "last", "done", "out", "next", "first",
-                                                                    "start")}
+                                                                    "start", "draft", "draft_len")}
         torch.cuda.synchronize()
 
     def greedy_continuations(self, steps: int) -> list[list[int]]:
@@ -117,17 +120,19 @@ class Workload:
         self.restore()
         return conts
 
-    def set_drafts(self, drafts: list[list[int]] | None) -> None:
-        """Load a draft per slot as ``SpecDecoder.filled`` does (draft position 0 = the first generated token)."""
-        dec, b = self.dec, SLOTS
-        for s in range(b):
-            d = [] if drafts is None else drafts[s][: dec.draft.size(1)]
-            dec.draft[s] = -1
-            if d:
-                dec.draft[s, : len(d)] = self.torch.tensor(d, device="cuda", dtype=self.torch.int32)
-            dec.draft_len[s] = len(d)
-        dec.next[:b] = 1
-        self.snapshot["next"] = dec.next[:b].clone()
+    def load_frame_drafts(self, frames: list[np.ndarray] | None) -> None:
+        """Give every slot a draft the way the transcriber does: per slot CTC frame argmaxes -> ``llm.Row.draft`` of its
+        (only) segment -> ``SpecDecoder.drafts`` -> ``SpecDecoder.filled``; ``frames`` None: no drafts (own tokens, the
+        seeded history searchable again).  The state after the load becomes the state ``restore`` returns to."""
+        pkg, dec, b = self.pkg, self.dec, SLOTS
+        self.restore()
+        rows = [pkg.llm.Row(index=s, segments=1, frames=None if frames is None else frames[s]) for s in range(b)]
+        dec.drafts = lambda j: rows[j].draft(0)
+        dec.filled(list(range(b)), list(range(b)))
+        dec.drafts = lambda j: None
+        if frames is None:
+            dec.first[:b] = self.first_history  # the own-token search sees the seeded history again
+        self.snapshot = {k: getattr(dec, k)[:b].clone() for k in self.snapshot}
         self.torch.cuda.synchronize()
 
     def restore(self):
@@ -141,16 +146,17 @@ class Workload:
         need = [x + 8 * (DRAFT + 1) + 2 for x in (lo, hi)]
         return sorted({min(self.dec.capacity, -(-n // 256) * 256) for n in range(need[0], need[1] + 256, 256)})
 
-    def run(self, steps: int) -> tuple[int, int]:
-        """``steps`` drafted steps in groups of ``sync_every`` replays with a host look after each group; returns
-        (tokens accepted, row-steps of running rows)."""
+    def run(self, steps: int, until_done: bool = False) -> tuple[int, int]:
+        """``steps`` drafted steps (``until_done``: until every slot has generated its budget, at most ``steps``) in
+        groups of ``sync_every`` replays with a host look after each group; returns (tokens accepted, row-steps of
+        running rows).  ``self.steps_run`` holds the steps replayed."""
         torch, dec, b = self.torch, self.dec, SLOTS
         start = self.snapshot["last"].cpu().numpy()
         last = dec.last[:b].cpu().numpy()
         done = dec.done[:b].cpu().numpy()
         tokens = row_steps = 0
         s = 0
-        while s < steps:
+        while s < steps and not (until_done and done.all()):
             n = min(dec.sync_every, steps - s)
             need = int(last.max()) + dec.sync_every * dec.step_tokens + 2
             keys = min(dec.capacity, -(-need // 256) * 256)
@@ -167,6 +173,7 @@ class Workload:
             if len(over):  # the slot's generation budget: finished as the host's repetition stop finishes rows
                 dec.done[torch.as_tensor(over, device="cuda")] = True
                 done = dec.done[:b].cpu().numpy()
+        self.steps_run = s
         return tokens, row_steps
 
 
@@ -487,18 +494,23 @@ def measured_traffic() -> int | None:
     return None
 
 
-def blas_threads() -> int:
+def host_cpu() -> tuple[int, str]:
+    """The cores this process may run on (``sched_getaffinity``) and the CPU's model name (``lscpu``)."""
+    cores = len(os.sched_getaffinity(0))
+    model = platform.processor() or "unknown"
     try:
-        from threadpoolctl import threadpool_info
-
-        counts = [int(p.get("num_threads", 1)) for p in threadpool_info() if p.get("user_api") == "blas"]
-        return max(counts) if counts else 1
+        text = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=30).stdout
+        model = next(line.split(":", 1)[1].strip() for line in text.splitlines() if line.startswith("Model name"))
     except Exception:
-        return os.cpu_count() or 1
+        pass
+    return cores, model
 
 
 def cpu_baseline(pkg, torch, w: Workload, seconds: float) -> dict:
-    """The numpy oracle's drafted step (fp32) on the host from the same post-prefill state, for about ``seconds``."""
+    """The numpy oracle's drafted step (fp32) on the host from the same post-prefill state, for about ``seconds``,
+    its BLAS on every core this process may use."""
+    from threadpoolctl import threadpool_limits
+
     from oracle import step as ostep
 
     spec = pkg.spec
@@ -508,30 +520,26 @@ def cpu_baseline(pkg, torch, w: Workload, seconds: float) -> dict:
     cap = dec.capacity
     k = dec.k[:, :b].float().cpu().numpy()
     v = dec.v[:, :b].float().cpu().numpy()
-    snap = {key: val.cpu().numpy().copy() for key, val in w.snapshot.items()}
-    state = {**snap, "draft": dec.draft[:b].cpu().numpy(), "draft_len": dec.draft_len[:b].cpu().numpy()}
+    state = {key: val.cpu().numpy().copy() for key, val in w.snapshot.items()}
     cfg = w.cfg
     npdec = ostep.NumpySpecDecoder(weights, cfg.num_layers, cfg.num_heads, cfg.rms_eps, dec.m.rope.cpu().numpy(), k,
                                    v, state, DRAFT, spec.NGRAM, spec.BEHIND, spec.AHEAD, spec.REACH, spec.SELF_WINDOW,
                                    spec.SELF_MIN, pkg.decode.LIMIT, pkg.llm.EOS)
+    cores, model = host_cpu()
     tokens = steps = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        need = int(state["last"].max()) + 8 * (DRAFT + 1) + 2
-        keys = min(cap, -(-need // 256) * 256)
-        tokens += npdec.step(keys)
-        steps += 1
-    elapsed = time.perf_counter() - t0
-    cpu = platform.processor() or "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            cpu = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
-    except Exception:
-        pass
-    return {"value": round(tokens / elapsed, 2), "unit": "verified tokens/s", "cores": blas_threads(),
+    with threadpool_limits(limits=cores, user_api="blas"):
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            need = int(state["last"].max()) + 8 * (DRAFT + 1) + 2
+            keys = min(cap, -(-need // 256) * 256)
+            tokens += npdec.step(keys)
+            steps += 1
+        elapsed = time.perf_counter() - t0
+    return {"value": round(tokens / elapsed, 2), "unit": "verified tokens/s", "cores": cores,
             "kind": "port", "sample": f"{steps} drafted steps of config 4 (8 slots x 5 tokens, 12 layers, fp32 numpy "
-                                      f"oracle) from the post-prefill state, {elapsed:.1f} s, {tokens} tokens",
-            "cpu": cpu}
+                                      f"oracle, tests/test_oracle_step.py pins it) from the post-prefill state, "
+                                      f"{elapsed:.1f} s, {tokens} tokens",
+            "cpu": model}
 
 
 def main() -> int:
@@ -596,26 +604,43 @@ def main() -> int:
 
     ctc = None
     if not args.no_extra:
-        # Config 5a: drafts from a synthetic CTC transcript = the greedy output with 10% random substitutions.
+        # Config 5a: drafts from a synthetic CTC transcript -- the greedy output with 10% of its tokens substituted,
+        # laid out as CTC frames -- through Row.draft and SpecDecoder.filled, over every slot's whole budget.
         with torch.inference_mode():
-            conts = w.greedy_continuations(GENERATE + 16)  # the whole 300-token budget of every slot
+            conts = w.greedy_continuations(GENERATE + 16)
             rng = np.random.default_rng(1005)
-            drafts = [[int(rng.integers(3, w.cfg.vocab_size)) if rng.random() < 0.1 else t for t in c] for c in conts]
-            w.set_drafts(drafts)
+            per_segment = pkg.llm.SEGMENT // pkg.llm.HOP
+            frames = [pkg.transcribe.frames_from_tokens([c], per_segment, rng, substitute=0.1,
+                                                        vocab=w.cfg.vocab_size) for c in conts]
+            w.load_frame_drafts(frames)
             w.run(args.warmup)
             w.restore()
             torch.cuda.synchronize()
             t1 = time.perf_counter()
-            ctc_tokens, ctc_rows = w.run(args.steps)
+            ctc_tokens, ctc_rows = w.run(10 * GENERATE, until_done=True)
             torch.cuda.synchronize()
             ctc_s = time.perf_counter() - t1
-            w.set_drafts(None)
-            w.restore()
-        ctc = {"workload": "config 5a: drafts = greedy output with 10% substitutions", "steps": args.steps,
-               "tokens": ctc_tokens, "tokens_per_s": round(ctc_tokens / ctc_s, 2),
-               "ms_per_step": round(ctc_s * 1e3 / args.steps, 4),
-               "tokens_per_row_step": round(ctc_tokens / max(ctc_rows, 1), 3)}
-        print(f"[bench] CTC drafts: {ctc_tokens} tokens in {ctc_s * 1e3:.1f} ms", file=sys.stderr, flush=True)
+            ctc_steps = w.steps_run
+            start = w.snapshot["last"].cpu().numpy()
+            out = w.dec.out[:SLOTS].cpu().numpy()
+            diverged = []
+            for s_, c in enumerate(conts):
+                got = out[s_, start[s_]: start[s_] + len(c)]
+                diff = np.flatnonzero(got[: len(c)] != np.asarray(c[: len(got)]))
+                diverged.append(int(diff[0]) if len(diff) else None)
+            w.load_frame_drafts(None)
+        ctc = {"workload": "config 5a: CTC frame drafts of the greedy output with 10% substitutions (Row.draft -> "
+                           "SpecDecoder.filled), every slot's 300-token budget",
+               "steps": ctc_steps, "tokens": ctc_tokens, "tokens_per_s": round(ctc_tokens / ctc_s, 2),
+               "ms_per_step": round(ctc_s * 1e3 / max(ctc_steps, 1), 4),
+               "tokens_per_row_step": round(ctc_tokens / max(ctc_rows, 1), 3),
+               "diverged_at": diverged,
+               "note": "diverged_at: per slot, the first generated position where the drafted run's token differs from "
+                       "the transcript's source (a greedy run with own-token drafts); after it the draft no longer "
+                       "matches and acceptance falls to own-token drafting (bf16 near-ties decided differently by "
+                       "steps of other shapes)"}
+        print(f"[bench] CTC drafts: {ctc_tokens} tokens in {ctc_steps} steps, {ctc_s * 1e3:.1f} ms, diverged at "
+              f"{diverged}", file=sys.stderr, flush=True)
     beams = None
     if not args.no_extra:
         with torch.inference_mode():

@@ -8,6 +8,9 @@ A drop-in for omniasr-trt's decode-step kernels (``omniasr_trt.kernels``) and th
 * ``decode``   -- ``GreedyDecoder``: static KV cache, HIP-graph steps, continuous-batching host loop;
 * ``spec``     -- ``SpecDecoder``: the drafted (speculative) greedy step;
 * ``beam``     -- ``BeamDecoder``: batched beam search over shared-context / pointer-indirected caches;
+* ``batching`` -- the continuous-batching scheduler, step-graph cache and packed weights the decoders share;
+* ``transcribe`` -- ``Transcriber``: segment contexts, the choice of decoder, CTC-frame drafts into the drafted
+  decoder (the reference's ``LLMTranscriber`` decoding side);
 * ``modeling`` -- the omniASR LLM decoder (fairseq2 parameter names) and its RoPE table;
 * ``llm``      -- streaming constants, the repetition stop, CTC-frame drafts.
 
@@ -21,11 +24,12 @@ _ALIAS = "omniasr_trt_amd"
 _sys.modules.setdefault(_ALIAS, _sys.modules[__name__])
 
 from . import _lib, kernels, llm, modeling  # noqa: E402
-from . import decode, spec  # noqa: E402
-from . import beam  # noqa: E402
+from . import batching, decode, spec  # noqa: E402
+from . import beam, transcribe  # noqa: E402
 
-for _name, _mod in (("_lib", _lib), ("kernels", kernels), ("llm", llm), ("modeling", modeling), ("decode", decode),
-                    ("spec", spec), ("beam", beam)):
+for _name, _mod in (("_lib", _lib), ("kernels", kernels), ("llm", llm), ("modeling", modeling),
+                    ("batching", batching), ("decode", decode), ("spec", spec), ("beam", beam),
+                    ("transcribe", transcribe)):
     _sys.modules.setdefault(f"{_ALIAS}.{_name}", _mod)
 
-__all__ = ["beam", "decode", "kernels", "llm", "modeling", "spec"]
+__all__ = ["batching", "beam", "decode", "kernels", "llm", "modeling", "spec", "transcribe"]

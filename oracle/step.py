@@ -4,7 +4,9 @@
 assembly, embedding gather, per layer RMSNorm -> qkv GEMM -> RoPE + append -> causal multi-query attention -> output
 projection -> RMSNorm -> gate|inner GEMM -> SiLU -> FFN output, final RMSNorm, LM head, log-softmax argmax and the
 acceptance.  Everything in float32 (numpy has no bf16 GEMM).  ``bench.py`` times it on the host cores as the CPU
-baseline of the verified-tokens/s metric; tests use it on small shapes.
+baseline of the verified-tokens/s metric.  Pinned by tests/test_oracle_step.py: on a small fp32 model, drafted
+decoding with perfect, noisy and no drafts gives the fp64 reference-order loop's tokens, and every step's verify
+logits agree with an fp64 forward over the same token sequence to fp32 precision.
 """
 
 from __future__ import annotations
@@ -67,6 +69,7 @@ class NumpySpecDecoder:
             gate, inner = np.split(gi, 2, axis=-1)
             h = (h + (inner * _silu(gate)) @ w[p + "ffn.output_proj.weight"].T).astype(F32)
         logits = _rms(h, w["llama_decoder.layer_norm.weight"], self.eps) @ w["final_proj.weight"].T
+        self.last_logits, self.last_tokens = logits, tokens  # the step's verify logits [B*T, V] and fed tokens [B, T]
         nxt = ov.log_softmax_argmax(logits, "f32").reshape(-1, t)
         before = s["last"].copy()
         ov.accept(tokens, nxt, s["out"], s["tok"], s["last"], s["done"], s["next"], s["start"], use, self.limit,

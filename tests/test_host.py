@@ -72,3 +72,22 @@ def test_bench_runs_one_gpu_only():
                        timeout=120, cwd=root)
     assert r.returncode == 2
     assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_synthetic_frames_give_back_each_segments_tokens(monkeypatch):
+    """transcribe.frames_from_tokens (the CTC stand-in of the tests and the benchmark): Row.draft of segment i
+    returns the tokens of the neighbouring frames' margin and then segment i's own, starting at ``before``."""
+    from omniasr_trt_amd.transcribe import frames_from_tokens
+
+    monkeypatch.setattr(llm, "SEGMENT", 100 * modeling.HOP)
+    rng = np.random.default_rng(4)
+    segments = [[int(x) for x in rng.integers(3, 50, n)] for n in (20, 7, 33, 0, 12)]
+    frames = frames_from_tokens(segments, 100, rng)
+    assert len(frames) == 500
+    row = llm.Row(index=0, segments=5, frames=frames)
+    for i, seg in enumerate(segments):
+        ids, before = row.draft(i)
+        assert ids[before: before + len(seg)] == seg, i
+    noisy = frames_from_tokens(segments, 100, np.random.default_rng(4), substitute=0.5, vocab=50)
+    ids, before = llm.Row(index=0, segments=5, frames=noisy).draft(2)
+    assert ids[before: before + 33] != segments[2] and len(ids[before: before + 33]) == 33

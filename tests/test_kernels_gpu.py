@@ -277,25 +277,34 @@ def _done_state(cuda, b, t, cap=64):
                 done=torch.ones(b, device=cuda, dtype=torch.bool))
 
 
+ARGMAX_MISMATCH_BOUND = 1e-3  # of all rows: kernel vs PyTorch's GPU op, lse-fragile rows included
+
+
 def test_argmax_matches_torch_on_the_gpu(cuda):
-    """Against PyTorch's own ``F.log_softmax(bf16).argmax`` on the same device: equal on every row except those whose
-    result hinges on the last bits of the log-sum-exp (flagged by the oracle), and equal to the oracle's."""
+    """Against PyTorch's own ``F.log_softmax(bf16).argmax`` on the same device, over 4000 rows of N(0, 1) and of
+    N(0, 3) logits [40, 10288] (the drafted step's shape): the kernel equals the oracle and PyTorch on every row
+    except those whose result hinges on the last bits of the log-sum-exp (flagged by the oracle), and the rows where
+    it differs from PyTorch -- fragile ones included -- are counted and stay below ARGMAX_MISMATCH_BOUND."""
     g = gen(1001)
-    fragile_total, rows = 0, 0
-    for batch in range(20):
-        x = torch.randn(40, 10288, generator=g).to(torch.bfloat16)
-        xd = x.to(cuda)
-        st = _done_state(cuda, 8, 5)
-        got = kernels.greedy_accept(xd, st["tokens"], st["out"], st["tok"], st["last"], st["done"], None, None, None,
-                                    8188, 2).view(-1).cpu().numpy()
-        want = F.log_softmax(xd, -1).argmax(-1).cpu().numpy()
-        fragile = ov.argmax_is_fragile(npf(x), "bf16")
-        oracle = ov.log_softmax_argmax(npf(x), "bf16")
-        assert not ((got != want) & ~fragile).any(), batch
-        assert not ((got != oracle) & ~fragile).any(), batch
-        fragile_total += int(fragile.sum())
-        rows += 40
-    say(f"argmax: {rows} rows, {fragile_total} flagged as lse-fragile")
+    for scale in (1.0, 3.0):
+        fragile_total = mismatches = rows = 0
+        for batch in range(100):
+            x = (torch.randn(40, 10288, generator=g) * scale).to(torch.bfloat16)
+            xd = x.to(cuda)
+            st = _done_state(cuda, 8, 5)
+            got = kernels.greedy_accept(xd, st["tokens"], st["out"], st["tok"], st["last"], st["done"], None, None,
+                                        None, 8188, 2).view(-1).cpu().numpy()
+            want = F.log_softmax(xd, -1).argmax(-1).cpu().numpy()
+            fragile = ov.argmax_is_fragile(npf(x), "bf16")
+            oracle = ov.log_softmax_argmax(npf(x), "bf16")
+            assert not ((got != want) & ~fragile).any(), batch
+            assert not ((got != oracle) & ~fragile).any(), batch
+            fragile_total += int(fragile.sum())
+            mismatches += int((got != want).sum())
+            rows += x.size(0)
+        say(f"argmax N(0, {scale:g}): {rows} rows, {fragile_total} lse-fragile, {mismatches} differ from PyTorch's GPU "
+            f"op")
+        assert mismatches <= ARGMAX_MISMATCH_BOUND * rows
 
 
 @pytest.mark.parametrize("v", [12, 10288, 10291])

@@ -11,6 +11,10 @@ drafted steps, with every kernel's inputs recorded and its effect checked agains
   equals ``oracle.verify.accept`` applied to the state before: the kept tokens are the argmaxes of the step's own
   logits, and every running slot advances by n + 1 in [1, 5] positions.
 
+Two phases of STEPS steps each: own-token drafting from the seeded history (the benchmark's main leg; the random
+model's argmax rarely follows a repeat, so about one token per step), then perfect drafts -- the run's own greedy
+tokens as CTC frames, loaded through ``Row.draft`` and ``SpecDecoder.filled`` -- where most proposals are kept.
+
 The decoder layer math between the kernels (GEMMs, norms) is torch's; what is checked here is the kernels at the
 shapes the benchmark times, inside the decoder, with the state they really see."""
 
@@ -73,68 +77,84 @@ def test_config4_drafted_steps(cuda, monkeypatch):
         rec["nxt"] = res.clone()
         return res
 
+    with torch.inference_mode():
+        # perfect drafts for the second phase: the run's own greedy tokens, as CTC frames through Row.draft -> filled
+        conts = w.greedy_continuations(3 * STEPS)
+        per_segment = pkg.llm.SEGMENT // pkg.llm.HOP
+        frames = [pkg.transcribe.frames_from_tokens([c], per_segment, np.random.default_rng(i))
+                  for i, c in enumerate(conts)]
     monkeypatch.setattr(kernels, "spec_prepare", prepare)
     monkeypatch.setattr(kernels, "rope_kv", rope)
     monkeypatch.setattr(kernels, "greedy_accept", accept)
     cs = npf(dec.m.rope)
     fragile_rows = 0
+    accepted = {}
     with torch.inference_mode():
-        for step in range(STEPS):
-            before = {name: host(getattr(dec, name)[:b]) for name in
-                      ("out", "draft", "draft_len", "last", "first", "next", "tok", "done", "start")}
-            keys = min(dec.capacity, -(-(int(before["last"].max()) + 8 * (bench.DRAFT + 1) + 2) // 256) * 256)
-            rec["rope"] = []
-            dec.step(b, keys)
-            torch.cuda.synchronize()
-            say(f"step {step}: keys {keys}, last {before['last'].tolist()}")
+        for phase in ("own tokens", "frame drafts"):
+            if phase == "frame drafts":
+                w.load_frame_drafts(frames)
+            accepted[phase] = 0
+            for step in range(STEPS):
+                before = {name: host(getattr(dec, name)[:b]) for name in
+                          ("out", "draft", "draft_len", "last", "first", "next", "tok", "done", "start")}
+                keys = min(dec.capacity, -(-(int(before["last"].max()) + 8 * (bench.DRAFT + 1) + 2) // 256) * 256)
+                rec["rope"] = []
+                dec.step(b, keys)
+                torch.cuda.synchronize()
+                say(f"step {step}: keys {keys}, last {before['last'].tolist()}")
 
-            # proposal and step assembly
-            tokens, pos, slots, lengths, use, start = ov.spec_prepare(
-                before["out"], before["draft"], before["draft_len"], before["last"], before["first"], before["next"],
-                before["tok"], before["done"], dec.capacity, bench.DRAFT, spec.NGRAM, spec.BEHIND, spec.AHEAD,
-                spec.REACH, 256, 256, spec.SELF_MIN)
-            got = [host(t) for t in rec["prepare"]]
-            for name, g, want in zip(("tokens", "pos", "slots", "lengths", "use_draft"), got,
-                                     (tokens, pos, slots, lengths, use)):
-                np.testing.assert_array_equal(g, want, err_msg=f"step {step}: {name}")
-            np.testing.assert_array_equal(host(dec.start[:b]), start)
+                # proposal and step assembly
+                tokens, pos, slots, lengths, use, start = ov.spec_prepare(
+                    before["out"], before["draft"], before["draft_len"], before["last"], before["first"], before["next"],
+                    before["tok"], before["done"], dec.capacity, bench.DRAFT, spec.NGRAM, spec.BEHIND, spec.AHEAD,
+                    spec.REACH, 256, 256, spec.SELF_MIN)
+                got = [host(t) for t in rec["prepare"]]
+                for name, g, want in zip(("tokens", "pos", "slots", "lengths", "use_draft"), got,
+                                         (tokens, pos, slots, lengths, use)):
+                    np.testing.assert_array_equal(g, want, err_msg=f"step {step}: {name}")
+                np.testing.assert_array_equal(host(dec.start[:b]), start)
 
-            # RoPE + append in the watched layers
-            assert len(rec["rope"]) == layers
-            for i in sorted(watch):
-                qkv, p, sl, q, (k_before, v_before), k_after, v_after = rec["rope"][i]
-                rows = host(sl)
-                cols = host(p)
-                n = len(rows)
-                # the oracle writes token j at column j of a small cache (its K/V rows only)
-                kc = np.zeros((b, dec.heads, n, dec.head_dim), dtype=np.float32)
-                vc = np.zeros_like(kc)
-                want_q = ov.rope_kv(npf(qkv), cs, cols, kc, vc, dec.heads, rows, np.arange(n), "bf16")
-                np.testing.assert_array_equal(npf(q), want_q, err_msg=f"step {step} layer {i}: q")
-                ri, ci = torch.as_tensor(rows, device=cuda), torch.as_tensor(cols, device=cuda)
-                np.testing.assert_array_equal(npf(k_after[ri, :, ci]), kc[rows, :, np.arange(n)])
-                np.testing.assert_array_equal(npf(v_after[ri, :, ci]), vc[rows, :, np.arange(n)])
-                # everything else untouched: put the written rows into the copy taken before, compare all of it
-                k_before[ri, :, ci] = k_after[ri, :, ci]
-                v_before[ri, :, ci] = v_after[ri, :, ci]
-                assert torch.equal(k_before, k_after) and torch.equal(v_before, v_after), f"step {step} layer {i}"
-            rec["rope"] = []
+                # RoPE + append in the watched layers
+                assert len(rec["rope"]) == layers
+                for i in sorted(watch):
+                    qkv, p, sl, q, (k_before, v_before), k_after, v_after = rec["rope"][i]
+                    rows = host(sl)
+                    cols = host(p)
+                    n = len(rows)
+                    # the oracle writes token j at column j of a small cache (its K/V rows only)
+                    kc = np.zeros((b, dec.heads, n, dec.head_dim), dtype=np.float32)
+                    vc = np.zeros_like(kc)
+                    want_q = ov.rope_kv(npf(qkv), cs, cols, kc, vc, dec.heads, rows, np.arange(n), "bf16")
+                    np.testing.assert_array_equal(npf(q), want_q, err_msg=f"step {step} layer {i}: q")
+                    ri, ci = torch.as_tensor(rows, device=cuda), torch.as_tensor(cols, device=cuda)
+                    np.testing.assert_array_equal(npf(k_after[ri, :, ci]), kc[rows, :, np.arange(n)])
+                    np.testing.assert_array_equal(npf(v_after[ri, :, ci]), vc[rows, :, np.arange(n)])
+                    # everything else untouched: put the written rows into the copy taken before, compare all of it
+                    k_before[ri, :, ci] = k_after[ri, :, ci]
+                    v_before[ri, :, ci] = v_after[ri, :, ci]
+                    assert torch.equal(k_before, k_after) and torch.equal(v_before, v_after), f"step {step} layer {i}"
+                rec["rope"] = []
 
-            # argmax + acceptance
-            logits = npf(rec["logits"])
-            nxt = host(rec["nxt"]).reshape(-1)
-            want = ov.log_softmax_argmax(logits, "bf16")
-            fragile = ov.argmax_is_fragile(logits, "bf16")
-            assert not ((nxt != want) & ~fragile).any(), f"step {step}: argmax"
-            fragile_rows += int(fragile.sum())
-            after = {name: host(getattr(dec, name)[:b]) for name in ("out", "tok", "last", "done", "next")}
-            o_out, o_tok, o_last, o_done, o_next = (before[n].copy() for n in ("out", "tok", "last", "done", "next"))
-            ov.accept(host(rec["tokens"]), nxt.reshape(b, -1), o_out, o_tok, o_last, o_done, o_next, start, use,
-                      pkg.decode.LIMIT, pkg.llm.EOS)
-            for name, o in (("out", o_out), ("tok", o_tok), ("last", o_last), ("done", o_done), ("next", o_next)):
-                np.testing.assert_array_equal(after[name], o, err_msg=f"step {step}: {name}")
-            advance = after["last"] - before["last"]
-            running = ~before["done"]
-            assert ((advance[running] >= 1) & (advance[running] <= bench.DRAFT + 1)).all(), advance
-            say(f"step {step}: accepted {advance.tolist()}")
-    say(f"config 4: {STEPS} steps checked; {fragile_rows} of {STEPS * b * (bench.DRAFT + 1)} argmax rows lse-fragile")
+                # argmax + acceptance
+                logits = npf(rec["logits"])
+                nxt = host(rec["nxt"]).reshape(-1)
+                want = ov.log_softmax_argmax(logits, "bf16")
+                fragile = ov.argmax_is_fragile(logits, "bf16")
+                assert not ((nxt != want) & ~fragile).any(), f"step {step}: argmax"
+                fragile_rows += int(fragile.sum())
+                after = {name: host(getattr(dec, name)[:b]) for name in ("out", "tok", "last", "done", "next")}
+                o_out, o_tok, o_last, o_done, o_next = (before[n].copy() for n in ("out", "tok", "last", "done", "next"))
+                ov.accept(host(rec["tokens"]), nxt.reshape(b, -1), o_out, o_tok, o_last, o_done, o_next, start, use,
+                          pkg.decode.LIMIT, pkg.llm.EOS)
+                for name, o in (("out", o_out), ("tok", o_tok), ("last", o_last), ("done", o_done), ("next", o_next)):
+                    np.testing.assert_array_equal(after[name], o, err_msg=f"step {step}: {name}")
+                advance = after["last"] - before["last"]
+                running = ~before["done"]
+                assert ((advance[running] >= 1) & (advance[running] <= bench.DRAFT + 1)).all(), advance
+                accepted[phase] += int(advance[running].sum())
+                say(f"{phase}, step {step}: accepted {advance.tolist()}")
+    rows_checked = 2 * STEPS * b * (bench.DRAFT + 1)
+    say(f"config 4: {2 * STEPS} steps checked; {fragile_rows} of {rows_checked} argmax rows lse-fragile; tokens accepted "
+        f"{accepted}")
+    # the greedy run's own tokens as drafts: most proposals are kept (several tokens per row-step)
+    assert accepted["frame drafts"] > 2 * STEPS * b
