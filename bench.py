@@ -558,6 +558,8 @@ def main() -> int:
     p.add_argument("--head-dim", type=int, default=128, help="--attention-only: head dim")
     p.add_argument("--beam", action="store_true", help="--attention-only: the beam attention of config 5b instead "
                    "(synthetic caches)")
+    p.add_argument("--prefill-only", action="store_true", help="only the causal prefill attention, 8 contexts x 2048 "
+                   "positions at 32 x 128 and at the real checkpoint's 8 x 512 (for counter runs)")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box has one MI355X and the step shards by slot with no exchange "
@@ -569,6 +571,15 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X", file=sys.stderr)
         return 2
+    if args.prefill_only:
+        with torch.inference_mode():
+            base = AttentionCaches(torch, layers=1, cap=2048)
+            small = time_prefill_real(pkg, torch, base)
+            real = time_prefill_real(pkg, torch, AttentionCaches(torch, layers=1, cap=2048, heads=8, dim=512))
+        print(json.dumps({"metric": "prefill attention TFLOP/s", "value": real["TFLOPs"], "unit": "TFLOP/s",
+                          "n_gpus": 1, "prefill_attention_8x2048x32x128": small,
+                          "prefill_attention_real_8x2048x8x512": real}), flush=True)
+        return 0
     if args.attention_only and args.beam:
         with torch.inference_mode():
             ref = copy_reference(torch)

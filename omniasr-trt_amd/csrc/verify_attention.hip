@@ -105,6 +105,15 @@ __device__ __forceinline__ void put_partial(float* p, float v, bool through) {
   else *p = v;
 }
 
+// Memory order of the merge tickets' fetch-adds.  Relaxed: the ordering rests on each wave's s_waitcnt before its
+// ticket (its write-through partial stores acknowledged at the coherence point) and on the merger's loads being
+// issued only after its ticket returned.  OMNI_TICKET_ACQ_REL=1 builds them as agent-scope acquire-release
+// operations instead (an L2 write-back before and an L2 invalidate after each, on gfx950).
+#ifndef OMNI_TICKET_ACQ_REL
+#define OMNI_TICKET_ACQ_REL 0
+#endif
+constexpr int kTicketOrder = OMNI_TICKET_ACQ_REL ? __ATOMIC_ACQ_REL : __ATOMIC_RELAXED;
+
 // Two floats (m, l) written through in one 8-byte agent-scope store.
 __device__ __forceinline__ void put_through2(float* p, float x, float y) {
   const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
@@ -251,7 +260,7 @@ __device__ __forceinline__ void finish_split(const AttnArgs& a, int b, int h, in
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   int* counter = &a.counters[b * a.H + h];
   int ticket = 0;
-  if (lane_id() == 0) ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane_id() == 0) ticket = __hip_atomic_fetch_add(counter, 1, kTicketOrder, __HIP_MEMORY_SCOPE_AGENT);
   ticket = __shfl(ticket, 0, kWave);
   if (ticket != nact - 1) return;
   merge_splits_fast<OutT>(a, b, h, nact);  // every split's partial, read at the coherence point
@@ -556,7 +565,7 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
   int* counter = &a.counters[b * a.H + h];
-  if (threadIdx.x == 0) s_ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) s_ticket = __hip_atomic_fetch_add(counter, 1, kTicketOrder, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   if (s_ticket != r.nact - 1) return;
   merge_splits_fast<uint16_t>(a, b, h, r.nact, w * 128, 128);  // each wave its slice
@@ -820,7 +829,7 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       int v = 0;
       if (lane == 0)
-        v = __hip_atomic_fetch_add(&a.counters[u0], kTicketFirst, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v = __hip_atomic_fetch_add(&a.counters[u0], kTicketFirst, kTicketOrder, __HIP_MEMORY_SCOPE_AGENT);
       tk0 = __builtin_amdgcn_readfirstlane(v);
     }
     st = SoftmaxState{-INFINITY, -INFINITY, 0.f};
@@ -852,7 +861,7 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
     if (__builtin_amdgcn_readfirstlane(first) == 0) {
       int tk = 0;
       if (lane == 0)
-        tk = __hip_atomic_fetch_add(&a.counters[u1], kTicketClaim, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        tk = __hip_atomic_fetch_add(&a.counters[u1], kTicketClaim, kTicketOrder, __HIP_MEMORY_SCOPE_AGENT);
       tk = __builtin_amdgcn_readfirstlane(tk);
       if (lane == 0) s_tk[1] = tk;
       if (tk == kTicketFirst) {
@@ -917,7 +926,7 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
     __builtin_amdgcn_s_waitcnt(0);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __syncthreads();
-    if (tid == 0) s_tk[1] = __hip_atomic_fetch_add(&a.counters[u1], kTicketSecond, __ATOMIC_RELAXED,
+    if (tid == 0) s_tk[1] = __hip_atomic_fetch_add(&a.counters[u1], kTicketSecond, kTicketOrder,
                                                    __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (s_tk[1] == kTicketClaim + kTicketFirst) {  // the first half came out in between: merge here

@@ -130,7 +130,7 @@ def greedy_reference(dec: Fp64Decoder, ctx: torch.Tensor, limit: int = MAX_GEN -
 
 @torch.inference_mode()
 def beam_reference(dec: Fp64Decoder, ctx: torch.Tensor, beams: int, length_norm: bool = False,
-                   limit: int = MAX_GEN - 4, margins: list | None = None) -> list[int]:
+                   limit: int = MAX_GEN - 4, margins: list | None = None, gaps: list | None = None) -> list[int]:
     """Beam search of one context [C, D] in the reference's order of computation (src/omniasr_trt/llm.py:205-254).
 
     ``beams`` hypotheses, each with its own K/V cache; at the first step only hypothesis 0 is live (the others
@@ -144,7 +144,8 @@ def beam_reference(dec: Fp64Decoder, ctx: torch.Tensor, beams: int, length_norm:
 
     ``margins``: if a list, receives per step the smallest gap between consecutive offers among the best
     ``beams`` + 1 finite ones (relative to their size): where it is tiny, another rounding of the same arithmetic
-    can choose other survivors or order them differently.
+    can choose other survivors or order them differently.  ``gaps``: the same smallest gaps, absolute (in score
+    units), for arithmetic whose error does not shrink with the scores' size (bf16 activations).
     """
     ctx = ctx.detach().to("cpu", torch.float64)
     c, n = ctx.size(0), beams
@@ -173,11 +174,15 @@ def beam_reference(dec: Fp64Decoder, ctx: torch.Tensor, beams: int, length_norm:
         order = np.argsort(-flat, kind="stable")  # best first, ties to the lower flat index
         pick = order[:n]
         top = flat[pick]
-        if margins is not None:
+        if margins is not None or gaps is not None:
             best = flat[order[: n + 1]]
             best = best[np.isfinite(best)]
-            gaps = np.abs(np.diff(best)) / np.maximum(np.abs(best[1:]), 1.0)
-            margins.append(float(gaps.min()) if gaps.size else math.inf)
+            diffs = np.abs(np.diff(best))
+            if margins is not None:
+                rel = diffs / np.maximum(np.abs(best[1:]), 1.0)
+                margins.append(float(rel.min()) if rel.size else math.inf)
+            if gaps is not None:
+                gaps.append(float(diffs.min()) if diffs.size else math.inf)
         parent, token = pick // cand.shape[1], pick % cand.shape[1]
         out, ended, scores = out[parent].copy(), ended[parent].copy(), scores[parent].copy()
         caches = [[(k.clone(), v.clone()) for k, v in caches[p]] for p in parent]
