@@ -101,7 +101,11 @@ size_t omni_verify_attention_workspace(int32_t rows, int32_t tokens, int32_t hea
  * rows <= 256 and rows * heads >= 128, one launch of rows*heads 8-wave workgroups: workgroup i takes the
  * first half of the i-th longest (head, row) and the second half of the i-th shortest, and the two halves
  * of each unit merge through the workspace and ``counters`` (``chunk`` unused; results do not depend on
- * timing).  Otherwise, or when ``flags`` has OMNI_ATTN_SPLIT_K, split-K as above.
+ * timing).  With bf16, head_dim 256 or 512, contiguous key rows and rows <= 64: split-K with a fixed
+ * budget of 256 workgroups (at least one per row) dealt to the rows of each head in proportion to their
+ * key counts, the last split of each (row, head) merging the others through ``counters`` (``chunk`` and
+ * OMNI_ATTN_SEPARATE_COMBINE unused; results do not depend on timing).  Otherwise, or when ``flags`` has
+ * OMNI_ATTN_SPLIT_K, split-K as above.
  * bf16: head_dim 128, 256 or 512 with contiguous key rows runs on MFMA (256 / 512: a workgroup of one wave per
  * 128 dimensions, the partial scores added through LDS), any other multiple of 8 on the vector ALUs; f32:
  * vector ALUs (fp32 products).  tokens: 1..16 (1..32 for bf16 head dims 256 / 512 with contiguous key rows).

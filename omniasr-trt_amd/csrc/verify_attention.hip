@@ -54,6 +54,8 @@ struct AttnArgs {
   int causal;        // 1: query i sees lengths + i keys (drafted step); 0: every query sees lengths keys (beams)
   int ctx_splits;    // key splits of the grid (= splits, or splits - 1 with a generated-keys split)
   int gen_split;     // partial slot of the beams' generated keys (merged with the key splits), or -1
+  int balanced;      // wide-head split-K with a fixed number of workgroups per head (see balanced_split)
+  int rows;          // rows of the launch (balanced split-K)
 };
 
 struct SplitRange {
@@ -120,10 +122,27 @@ __device__ __forceinline__ void put_through2(float* p, float x, float y) {
   __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Four floats (16 bytes) written through to the coherence point as two 8-byte agent-scope stores.
-__device__ __forceinline__ void put_through4c(float* p, f32x4_t v) {
-  put_through2(p, v[0], v[1]);
-  put_through2(p + 2, v[2], v[3]);
+// Four floats of a partial written through to the coherence point: element ``at`` of the partial buffer ``base``
+// (wave-uniform).  One 16-byte store with the agent-scope cache policy (SC1: through the L2 to the device's
+// coherence point), issued through a buffer resource over ``base``; the offset is 32-bit (the launchers refuse
+// workspaces of 4 GiB and more).  OMNI_THROUGH16=0 builds the earlier form, two 8-byte agent-scope atomic stores.
+#ifndef OMNI_THROUGH16
+#define OMNI_THROUGH16 1
+#endif
+constexpr int kPolicySc1 = 16;  // buffer instruction cache policy bits: SC1
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const float* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, -1, 0x00020000);
+}
+
+__device__ __forceinline__ void put_through4(float* base, int64_t at, f32x4_t v) {
+#if OMNI_THROUGH16
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), partial_rsrc(base), (uint32_t)at * 4u, 0,
+                                         kPolicySc1);
+#else
+  put_through2(base + at, v[0], v[1]);
+  put_through2(base + at + 2, v[2], v[3]);
+#endif
 }
 
 // Partial slot of the q-th partial to merge: the row's key splits, then the generated-keys slot if any.
@@ -171,24 +190,31 @@ __device__ void merge_splits(const AttnArgs& a, int b, int h, int nact) {
 // The in-kernel merge by the row's last split: lane l owns the floats f = 1024p + 256r + 4l (query f / D) of the
 // row's T x D output block, and every load of a batch of up to 8 partials x 1024 floats is in flight at once (the
 // tile registers are free by then), so a typical merge is one memory round trip.
-__device__ __forceinline__ f32x4_t get_through4(const float* p) {
+__device__ __forceinline__ f32x4_t get_through4(const float* base, int64_t at) {
+#if OMNI_THROUGH16
+  return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(partial_rsrc(base), (uint32_t)at * 4u, 0,
+                                                                           kPolicySc1));
+#else
+  const float* p = base + at;
   const uint64_t lo = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
   const uint64_t hi = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)) + 1, __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
   return f32x4_t{__uint_as_float((uint32_t)lo), __uint_as_float((uint32_t)(lo >> 32)),
                  __uint_as_float((uint32_t)hi), __uint_as_float((uint32_t)(hi >> 32))};
+#endif
 }
 
 template <typename OutT>
-__device__ void merge_splits_fast(const AttnArgs& a, int b, int h, int nact, int d0 = 0, int dw = -1) {
+__device__ void merge_splits_fast(const AttnArgs& a, int b, int h, int nact, int d0 = 0, int dw = -1,
+                                  int64_t first_slot = -1) {
   constexpr int kS = 8, kR = 3;
   const int lane = lane_id();
   const int T = a.T, D = a.D;
   if (dw < 0) dw = D;  // dimensions d0 .. d0 + dw - 1 of every query (dw a multiple of 4)
   const int nf = T * dw;
   const int nq = nact + (a.gen_split >= 0 ? 1 : 0);
-  const int64_t split0 = ((int64_t)b * a.H + h) * a.splits;
+  const int64_t split0 = first_slot >= 0 ? first_slot : ((int64_t)b * a.H + h) * a.splits;
   OutT* out = reinterpret_cast<OutT*>(a.out);
   for (int f0 = 0; f0 < nf; f0 += kR * 256) {
     float top[kR], den[kR];
@@ -217,7 +243,7 @@ __device__ void merge_splits_fast(const AttnArgs& a, int b, int h, int nact, int
                                                   __HIP_MEMORY_SCOPE_AGENT);
             mv[sq][r] = __uint_as_float((uint32_t)ml);
             lv[sq][r] = __uint_as_float((uint32_t)(ml >> 32));
-            ov[sq][r] = get_through4(a.part_o + slot * D + d0 + (f - t * dw));
+            ov[sq][r] = get_through4(a.part_o, slot * D + d0 + (f - t * dw));
           }
         }
       }
@@ -394,8 +420,9 @@ __global__ __launch_bounds__(64, 2) void verify_attn_mfma_kernel(AttnArgs a) {
     for (int gg = 0; gg < NG; ++gg) {
       float* po = a.part_o + (base + t) * D + gg * 128 + c * 8;
       if (through) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) put_partial(po + e, o[gg * 8 + e][i], true);
+        const int64_t at = (base + t) * D + gg * 128 + c * 8;
+        put_through4(a.part_o, at, f32x4_t{o[gg * 8 + 0][i], o[gg * 8 + 1][i], o[gg * 8 + 2][i], o[gg * 8 + 3][i]});
+        put_through4(a.part_o, at + 4, f32x4_t{o[gg * 8 + 4][i], o[gg * 8 + 5][i], o[gg * 8 + 6][i], o[gg * 8 + 7][i]});
       } else {
         reinterpret_cast<f32x4_t*>(po)[0] = f32x4_t{o[gg * 8 + 0][i], o[gg * 8 + 1][i], o[gg * 8 + 2][i],
                                                     o[gg * 8 + 3][i]};
@@ -411,6 +438,66 @@ __global__ __launch_bounds__(64, 2) void verify_attn_mfma_kernel(AttnArgs a) {
   finish_split<uint16_t>(a, b, h, r.nact);
 }
 
+// Balanced split-K for wide heads: a fixed budget of ``a.splits`` workgroups per head (about two per CU in all) is
+// dealt to the rows in proportion to their tile counts -- one to every row, the rest by the largest remainder of
+// (budget - rows) x tiles / total tiles, ties to the lower row -- so every workgroup streams about the same number
+// of tiles whatever the rows' lengths.  Workgroup j of a head works on split k of row b, one of the row's nact
+// splits (tiles dealt round-robin over them, as in split-K); the partials of a head's workgroups take the head's
+// a.splits slots in workgroup order, so a unit's splits have consecutive slots from ``first``.  Every workgroup
+// computes the same deal from the rows' lengths (rows <= kBalancedMaxRows).  b < 0: no work (every row empty).
+constexpr int kBalancedMaxRows = 64;
+
+struct BalancedSplit {
+  int b, k, nact, first;
+};
+
+__device__ BalancedSplit balanced_split(const AttnArgs& a, int j) {
+  __shared__ int nt[kBalancedMaxRows], wk[kBalancedMaxRows], rem[kBalancedMaxRows];
+  __shared__ int s_total, s_given;
+  const int tid = threadIdx.x, rows = a.rows, budget = a.splits;  // the launcher ensures rows <= blockDim.x
+  if (tid < rows) nt[tid] = (int)((split_range(a, tid, 0).total + 31) >> 5);
+  __syncthreads();
+  if (tid == 0) {
+    int total = 0;
+    for (int b = 0; b < rows; ++b) total += nt[b];
+    s_total = total;
+  }
+  __syncthreads();
+  const int total = s_total, spare = budget - rows;
+  if (tid < rows) {
+    const int64_t share = total > 0 ? (int64_t)spare * nt[tid] : 0;
+    wk[tid] = 1 + (total > 0 ? (int)(share / total) : 0);
+    rem[tid] = total > 0 ? (int)(share % total) : 0;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int given = 0;
+    for (int b = 0; b < rows; ++b) given += wk[b];
+    s_given = given;
+  }
+  __syncthreads();
+  const int left = total > 0 ? budget - s_given : 0;  // < rows: one more to the rows of the largest remainders
+  int extra = 0;
+  if (tid < rows) {
+    int rank = 0;
+    for (int o = 0; o < rows; ++o) rank += rem[o] > rem[tid] || (rem[o] == rem[tid] && o < tid);
+    extra = rank < left;
+  }
+  __syncthreads();
+  if (tid < rows) wk[tid] += extra;
+  __syncthreads();
+  BalancedSplit out{-1, 0, 1, 0};
+  int first = 0;
+  for (int b = 0; b < rows; ++b) {
+    if (j < first + wk[b]) {
+      out = BalancedSplit{b, j - first, wk[b], first};
+      break;
+    }
+    first += wk[b];
+  }
+  return out;
+}
+
 // Split-K for head dims past 128 (256, 512): one workgroup of D/128 waves per (split, head, row), wave w holding
 // dimensions 128w .. 128w + 127 of q, K, V and O.  Each wave reads its slice of a tile (32 keys x 256 bytes of K
 // and of V; two tiles in flight, the register budget of the 128-dimension kernel), its partial scores go to LDS,
@@ -422,14 +509,30 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
   constexpr int NSL = D / 128;
   __shared__ float sx[2][NSL][G][kWave * 8];  // partial scores of a tile by slice and query group, double-buffered
   __shared__ int s_ticket;
-  const int sp = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const SplitRange r = split_range(a, b, sp);
-  if (sp >= r.nact) return;  // uniform over the workgroup
-  const int lane = lane_id(), w = threadIdx.x / kWave, c = lane & 15, g = lane >> 4;
+  const int h = blockIdx.y;
+  int sp, b;
+  SplitRange r;
+  int64_t slot0;  // partial slot of the unit's first split
+  if (a.balanced) {
+    const BalancedSplit bs = balanced_split(a, blockIdx.x);
+    if (bs.b < 0) return;  // uniform over the workgroup
+    b = bs.b;
+    sp = bs.k;
+    r = split_range(a, b, 0);
+    r.nact = bs.nact;
+    slot0 = (int64_t)h * a.splits + bs.first;
+  } else {
+    sp = blockIdx.x;
+    b = blockIdx.z;
+    r = split_range(a, b, sp);
+    if (sp >= r.nact) return;  // uniform over the workgroup
+    slot0 = ((int64_t)b * a.H + h) * a.splits;
+  }
+  const int lane = lane_id(), sl = threadIdx.x / kWave, c = lane & 15, g = lane >> 4;  // sl: this wave's slice
   const int T = a.T;
 
   // Query group u holds queries 16u .. 16u + 15 of the row.  B operand of the slice's S^T = K Q^T: lane (c, g) holds
-  // q[16u + c][128w + 32s + 8g .. + 7].
+  // q[16u + c][128 sl + 32s + 8g .. + 7].
   u32x4_t qop[G][4];
   SoftmaxState st[G];
   f32x4_t o[G][8];
@@ -438,7 +541,7 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
   for (int u = 0; u < G; ++u) {
     const int qi = 16 * u + c;
     const uint16_t* qrow =
-        reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)(b * T + qi) * a.H + h) * D + w * 128 + g * 8;
+        reinterpret_cast<const uint16_t*>(a.q) + ((int64_t)(b * T + qi) * a.H + h) * D + sl * 128 + g * 8;
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2)
       qop[u][s2] = qi < T ? *reinterpret_cast<const u32x4_t*>(qrow + s2 * 32) : u32x4_t{0u, 0u, 0u, 0u};
@@ -449,12 +552,13 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
     lim_c[u] = (int)(own < r.total ? own : r.total);
   }
 
+  // The split's tiles are k = 0 .. ntot - 1: tile first + k nact of the row.
   const int64_t row_tiles = (r.total + 31) >> 5;
   const int64_t first = sp;
   const int64_t ntot = first < row_tiles ? (row_tiles - first + r.nact - 1) / r.nact : 0;
   // The launcher sends only caches with contiguous key rows (s_pos == D) here.
-  const char* kt = reinterpret_cast<const char*>(a.k) + (b * a.s_row + h * a.s_head + first * 32 * D) * 2 + w * 256;
-  const char* vt = reinterpret_cast<const char*>(a.v) + (b * a.s_row + h * a.s_head + first * 32 * D) * 2 + w * 256;
+  const char* kt = reinterpret_cast<const char*>(a.k) + (b * a.s_row + h * a.s_head + first * 32 * D) * 2 + sl * 256;
+  const char* vt = reinterpret_cast<const char*>(a.v) + (b * a.s_row + h * a.s_head + first * 32 * D) * 2 + sl * 256;
   const int64_t tile_bytes = (int64_t)r.nact * 32 * D * 2;
   const int64_t last_key = a.cache_len - 1;
   auto load_k = [&](KVTile<128>& t, int64_t k) {
@@ -468,7 +572,7 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
     for (int u = 0; u < G; ++u) {
       float sv[8];
       tile_scores<128>(t, qop[u], sv);
-      float* mine = &sx[k & 1][w][u][lane * 8];
+      float* mine = &sx[k & 1][sl][u][lane * 8];
       *reinterpret_cast<f32x4_t*>(mine) = f32x4_t{sv[0], sv[1], sv[2], sv[3]};
       *reinterpret_cast<f32x4_t*>(mine + 4) = f32x4_t{sv[4], sv[5], sv[6], sv[7]};
     }
@@ -511,7 +615,7 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
 
   // ---- finish: per-query sums (the same in every wave), then the output slice or this split's partial slice
   const bool direct = r.nact == 1 && a.gen_split < 0;
-  const int64_t base = (((int64_t)b * a.H + h) * a.splits + sp) * T;
+  const int64_t base = (slot0 + sp) * T;
 #pragma unroll
   for (int u = 0; u < G; ++u) {
     float l_tot = st[u].l_run + __shfl_xor(st[u].l_run, 16, kWave);
@@ -529,7 +633,7 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
         u32x4_t wv;
 #pragma unroll
         for (int q2 = 0; q2 < 4; ++q2) wv[q2] = pack_bf16x2(o[u][2 * q2][i] / div, o[u][2 * q2 + 1][i] / div);
-        *reinterpret_cast<u32x4_t*>(out + ((int64_t)(b * T + t) * a.H + h) * D + w * 128 + c * 8) = wv;
+        *reinterpret_cast<u32x4_t*>(out + ((int64_t)(b * T + t) * a.H + h) * D + sl * 128 + c * 8) = wv;
       }
       continue;
     }
@@ -537,19 +641,20 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * u + 4 * g + i;
       if (t >= T) continue;
-      float* po = a.part_o + (base + t) * D + w * 128 + c * 8;
+      float* po = a.part_o + (base + t) * D + sl * 128 + c * 8;
       const f32x4_t x0 = f32x4_t{o[u][0][i], o[u][1][i], o[u][2][i], o[u][3][i]};
       const f32x4_t x1 = f32x4_t{o[u][4][i], o[u][5][i], o[u][6][i], o[u][7][i]};
       if (a.separate) {
         reinterpret_cast<f32x4_t*>(po)[0] = x0;
         reinterpret_cast<f32x4_t*>(po)[1] = x1;
       } else {
-        put_through4c(po, x0);
-        put_through4c(po + 4, x1);
+        const int64_t at = (base + t) * D + sl * 128 + c * 8;
+        put_through4(a.part_o, at, x0);
+        put_through4(a.part_o, at + 4, x1);
       }
     }
     const int tc = 16 * u + c;
-    if (w == 0 && g == 0 && tc < T) {
+    if (sl == 0 && g == 0 && tc < T) {
       if (a.separate) {
         a.part_ml[(base + tc) * 2] = st[u].m_ref;
         a.part_ml[(base + tc) * 2 + 1] = l_tot;
@@ -568,7 +673,7 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
   if (threadIdx.x == 0) s_ticket = __hip_atomic_fetch_add(counter, 1, kTicketOrder, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   if (s_ticket != r.nact - 1) return;
-  merge_splits_fast<uint16_t>(a, b, h, r.nact, w * 128, 128);  // each wave its slice
+  merge_splits_fast<uint16_t>(a, b, h, r.nact, sl * 128, 128, slot0);  // the last split merges; each wave its slice
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -597,7 +702,7 @@ __device__ __forceinline__ PartialItem get_partial(const AttnArgs& a, int64_t sl
   const uint64_t ml = __hip_atomic_load(reinterpret_cast<uint64_t*>(a.part_ml + (slot_base * a.T + t) * 2),
                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return PartialItem{__uint_as_float((uint32_t)ml), __uint_as_float((uint32_t)(ml >> 32)),
-                     get_through4(a.part_o + (slot_base * a.T + t) * a.D + d)};
+                     get_through4(a.part_o, (slot_base * a.T + t) * a.D + d)};
 }
 
 // Up to three partials of one output item merged and written (bf16).
@@ -821,7 +926,7 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
       for (int idx = lane; idx < T * (D / 4); idx += kWave) {
         const int t = idx / (D / 4), d = (idx - t * (D / 4)) * 4;
         const PartialItem m0 = merge_slots<kWgWaves>(po, pm, pl, T, D, t, d);
-        put_through4c(a.part_o + (sb * T + t) * D + d, m0.o);
+        put_through4(a.part_o, (sb * T + t) * D + d, m0.o);
         if (d == 0) put_through2(a.part_ml + (sb * T + t) * 2, m0.m, m0.l);
       }
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -919,7 +1024,7 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
     if (has_item) {
       m1 = merge_slots<kWgWaves>(po, pm, pl, T, D, item_t, item_d);
       const int64_t sb = (int64_t)u1 * slots + 1;
-      put_through4c(a.part_o + (sb * T + item_t) * D + item_d, m1.o);
+      put_through4(a.part_o, (sb * T + item_t) * D + item_d, m1.o);
       if (item_d == 0) put_through2(a.part_ml + (sb * T + item_t) * 2, m1.m, m1.l);
     }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -1181,17 +1286,48 @@ extern "C" int32_t omni_verify_attention_chunk(int32_t rows, int32_t tokens, int
 
 static size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
+// Partials are addressed with 32-bit byte offsets from the workspace base.
+static constexpr size_t kMaxWorkspace = (size_t)1 << 32;
+
 // Partial slots per unit in the workspace: split-K at this chunk, or a unit's two halves.
 static size_t attn_slots(int keys, int chunk) {
   const int splits = attn_splits(keys, chunk);
   return (size_t)(splits > 2 ? splits : 2);
 }
 
+// Balanced split-K for wide heads (bf16, head dim 256 / 512): workgroups per head.  OMNI_WIDE_WGS in all, one per CU
+// (measured at 8 rows x 8 heads x 512, T = 5: 42.1 us against 49.5 us with two per CU and 58.2 us with four), and
+// at least one per row.
+#ifndef OMNI_WIDE_WGS
+#define OMNI_WIDE_WGS 256
+#endif
+static int balanced_budget(int rows, int heads) {
+  const int per_head = OMNI_WIDE_WGS / heads;
+  return per_head > rows ? per_head : rows;
+}
+
+static bool balanced_shape(int32_t rows, int32_t heads, int32_t head_dim) {
+  // rows <= kBalancedMaxRows <= the workgroup's threads (one per row while the deal is computed)
+  return (head_dim == 256 || head_dim == 512) && rows <= kBalancedMaxRows && balanced_budget(rows, heads) <= 65535;
+}
+
+// Partial items (T x D floats and their (m, l)) the workspace holds: split-K slots per (row, head) -- a unit's splits
+// or its two halves -- or, for the balanced wide-head split-K, the heads' workgroup slots.
+static size_t attn_partial_items(int32_t rows, int32_t tokens, int32_t heads, int32_t head_dim, int32_t keys,
+                                 int32_t chunk) {
+  size_t units = (size_t)rows * heads * attn_slots(keys, chunk) * tokens;
+  if (balanced_shape(rows, heads, head_dim)) {
+    const size_t wide = (size_t)heads * balanced_budget(rows, heads) * tokens;
+    units = units > wide ? units : wide;
+  }
+  return units;
+}
+
 extern "C" size_t omni_verify_attention_workspace(int32_t rows, int32_t tokens, int32_t heads,
                                                   int32_t head_dim, int32_t keys, int32_t chunk) {
   if (rows <= 0 || tokens <= 0 || heads <= 0 || head_dim <= 0 || keys <= 0) return 0;
   if (chunk <= 0) chunk = omni_verify_attention_chunk(rows, tokens, heads, head_dim, keys);
-  const size_t units = (size_t)rows * heads * attn_slots(keys, chunk) * tokens;
+  const size_t units = attn_partial_items(rows, tokens, heads, head_dim, keys, chunk);
   return align256(units * head_dim * sizeof(float)) + align256(units * 2 * sizeof(float));
 }
 
@@ -1276,13 +1412,14 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
   if (!q || !k_cache || !v_cache || !lengths || !out || !workspace || !counters) return OMNI_ERR_INVALID;
   if (chunk == 0) chunk = omni_verify_attention_chunk(rows, tokens, heads, head_dim, keys);
   if (chunk <= 0 || chunk % 32 != 0) return OMNI_ERR_INVALID;
-  if (workspace_bytes < omni_verify_attention_workspace(rows, tokens, heads, head_dim, keys, chunk))
-    return OMNI_ERR_WORKSPACE;
+  const size_t need = omni_verify_attention_workspace(rows, tokens, heads, head_dim, keys, chunk);
+  if (need >= kMaxWorkspace) return OMNI_ERR_SHAPE;  // partial offsets are 32-bit
+  if (workspace_bytes < need) return OMNI_ERR_WORKSPACE;
   if (((uintptr_t)workspace & 255u) != 0) return OMNI_ERR_WORKSPACE;
   if (!attention_aligned(q, out, k_cache, v_cache, stride_row, stride_head, stride_pos, head_dim, dtype))
     return OMNI_ERR_INVALID;
   const int splits = attn_splits(keys, chunk);
-  const size_t units = (size_t)rows * heads * attn_slots(keys, chunk) * tokens;
+  const size_t units = attn_partial_items(rows, tokens, heads, head_dim, keys, chunk);
   AttnArgs a;
   a.q = q;
   a.k = k_cache;
@@ -1306,6 +1443,8 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
   a.causal = 1;
   a.ctx_splits = splits;
   a.gen_split = -1;
+  a.balanced = 0;
+  a.rows = rows;
   hipStream_t s = (hipStream_t)stream;
   const bool wg = dtype == OMNI_BF16 && head_dim == 128 && stride_pos == head_dim && tokens <= kWgMaxT &&
                   rows <= kPairMaxRows && !(flags & OMNI_ATTN_SPLIT_K) && (int64_t)rows * heads >= kWgMinUnits &&
@@ -1317,6 +1456,24 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
     const int slots = (int)attn_slots(keys, chunk);
     verify_attn_pair_kernel<128><<<rows * heads, 64 * kWgWaves, pair_lds_bytes(tokens, head_dim), s>>>(a, rows,
                                                                                                      slots);
+    return omni_launch_status();
+  }
+  if (dtype == OMNI_BF16 && stride_pos == head_dim && balanced_shape(rows, heads, head_dim) &&
+      !(flags & OMNI_ATTN_SPLIT_K)) {
+    // wide heads: a fixed budget of workgroups per head dealt to the rows by length, merged in the kernel
+    a.balanced = 1;
+    a.splits = balanced_budget(rows, heads);
+    a.ctx_splits = 1;
+    a.chunk = (keys + 31) / 32 * 32;  // every key of a row is in its (one) range; the deal splits it
+    a.separate = 0;
+    dim3 grid(a.splits, heads, 1);
+    if (head_dim == 256) {
+      if (tokens > 16) verify_attn_slice_kernel<256, 2><<<grid, 128, 0, s>>>(a);
+      else verify_attn_slice_kernel<256, 1><<<grid, 128, 0, s>>>(a);
+    } else {
+      if (tokens > 16) verify_attn_slice_kernel<512, 2><<<grid, 256, 0, s>>>(a);
+      else verify_attn_slice_kernel<512, 1><<<grid, 256, 0, s>>>(a);
+    }
     return omni_launch_status();
   }
   st = launch_attention(a, rows, dtype, s);
@@ -1746,8 +1903,9 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
     return OMNI_ERR_INVALID;
   if (chunk == 0) chunk = omni_verify_attention_chunk(groups, beams, heads, head_dim, ctx_keys);
   if (chunk <= 0 || chunk % 32 != 0) return OMNI_ERR_INVALID;
-  if (workspace_bytes < omni_beam_attention_workspace(groups, beams, heads, head_dim, ctx_keys, chunk))
-    return OMNI_ERR_WORKSPACE;
+  const size_t need = omni_beam_attention_workspace(groups, beams, heads, head_dim, ctx_keys, chunk);
+  if (need >= kMaxWorkspace) return OMNI_ERR_SHAPE;  // partial offsets are 32-bit
+  if (workspace_bytes < need) return OMNI_ERR_WORKSPACE;
   if (((uintptr_t)workspace & 255u) != 0) return OMNI_ERR_WORKSPACE;
   if (!attention_aligned(q, out, k_ctx, v_ctx, ctx_row, ctx_head, ctx_pos, head_dim, dtype)) return OMNI_ERR_INVALID;
   const int ctx_splits = attn_splits(ctx_keys, chunk);
@@ -1776,6 +1934,8 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
   a.causal = 0;
   a.ctx_splits = ctx_splits;
   a.gen_split = ctx_splits;
+  a.balanced = 0;
+  a.rows = groups;
   hipStream_t s = (hipStream_t)stream;
   const bool halves = dtype == OMNI_BF16 && head_dim == 128 && ctx_pos == head_dim && beams <= kWgMaxT &&
                       groups <= kPairMaxRows && counters != nullptr && (int64_t)groups * heads >= kWgMinUnits &&

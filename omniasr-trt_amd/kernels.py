@@ -31,11 +31,11 @@ import torch
 
 from . import _lib
 
-# Launch settings of draft_attention / decode_attention.  ``split_k``: always split the keys over waves of their
-# own (otherwise the library runs one 8-wave workgroup per (head, row) when rows x heads cover the CUs, merging in
-# LDS).  Split-K only: ``chunk`` keys per split (0: the library's choice for the launch shape), ``separate``: merge
-# the splits in a second launch (else the last split of each row and head merges them, reading the other splits'
-# partials through to the coherence point -- measured slower than the second launch).
+# Launch settings of draft_attention / decode_attention.  ``split_k``: always plain split-K (otherwise the library
+# runs the balanced halves kernel for head dim 128 when rows x heads cover the CUs, and for head dims 256 / 512 a
+# split-K whose workgroup budget is dealt to the rows by length, merged in the kernel).  Plain split-K only: ``chunk``
+# keys per split (0: the library's choice for the launch shape), ``separate``: merge the splits in a second launch
+# (else the last split of each row and head merges them, reading the other splits' partials at the coherence point).
 DRAFT_ATTN = {"chunk": 0, "separate": True, "split_k": False}
 ATTN = {"chunk": 0, "separate": True, "split_k": False}
 

@@ -37,12 +37,15 @@ def test_abi_version_and_status_text():
 
 def test_workspace_and_split_queries():
     lib = _lib.load()
-    for rows, t, h, d, keys in ((8, 5, 32, 128, 2560), (8, 1, 8, 512, 2048), (1, 9, 32, 128, 1280), (4, 3, 2, 16, 256)):
+    for rows, t, h, d, keys in ((8, 5, 32, 128, 2560), (8, 1, 8, 512, 2048), (1, 9, 32, 128, 1280), (4, 3, 2, 16, 256),
+                                (1, 5, 2, 512, 256), (64, 3, 4, 256, 1024)):
         chunk = lib.omni_verify_attention_chunk(rows, t, h, d, keys)
         assert chunk % 32 == 0 and 32 <= chunk <= max(64, -(-keys // 32) * 32)
         splits = -(-keys // chunk)
         slots = max(splits, 2)  # split-K partials, or a unit's two halves
         units = rows * h * slots * t
+        if d in (256, 512) and rows <= 64:  # the wide heads' balanced split-K: 256 workgroup slots over the heads
+            units = max(units, h * max(rows, 256 // h) * t)
         want = -(-units * d * 4 // 256) * 256 + -(-units * 2 * 4 // 256) * 256
         assert lib.omni_verify_attention_workspace(rows, t, h, d, keys, 0) == want
     # config 3: 8 rows x 32 heads, keys 2560 -> 320 keys for 2048 waves, capped at 8 tiles per split

@@ -236,6 +236,57 @@ def test_verify_attention_halves_shapes(cuda, rows, heads):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("rows,heads,d,t", [(8, 8, 512, 5), (1, 8, 512, 9), (64, 2, 512, 1), (8, 4, 256, 5),
+                                             (3, 8, 512, 16)])
+def test_verify_attention_wide_balanced(cuda, rows, heads, d, t):
+    """Wide heads (256 / 512) by default run split-K with a fixed workgroup budget per head dealt to the rows by
+    their lengths, merged in the kernel: against the oracle and against plain split-K (forced), with empty rows,
+    rows shorter than a tile, one row (every workgroup of a head on it) and the most rows the deal takes (64)."""
+    g = gen(rows * 31 + d + t)
+    lengths = torch.randint(0, 1200, (rows,), generator=g)
+    lengths[::5] = 0
+    lengths[1::7] = torch.randint(1, 31, (len(lengths[1::7]),), generator=g)
+    keys = -(-(int(lengths.max()) + t) // 256) * 256
+    a = _attn_case(cuda, torch.bfloat16, rows, heads, d, t, keys, lengths, keys, rows + d, BF16_TOL)
+    b = _attn_case(cuda, torch.bfloat16, rows, heads, d, t, keys, lengths, keys, rows + d, BF16_TOL, split_k=True)
+    torch.testing.assert_close(a.float(), b.float(), atol=1e-2, rtol=1e-2)
+    torch.cuda.synchronize()
+    assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
+    c = _attn_case(cuda, torch.bfloat16, rows, heads, d, t, keys, lengths, keys, rows + d, BF16_TOL)
+    assert torch.equal(a, c)  # the deal and the merge order are fixed: the same bits every call
+
+
+def test_verify_attention_wide_graph_replays(cuda):
+    """The real checkpoint's shape (8 rows x 8 heads x 512, T = 5) captured once and replayed with new lengths written
+    in place: every replay equals the eager call bit for bit, and the tickets are left zero."""
+    g = gen(88)
+    b, h, d, t, cap = 8, 8, 512, 5, 2560
+    kc = torch.randn(b, h, cap, d, generator=g).to(torch.bfloat16).to(cuda)
+    vc = torch.randn(b, h, cap, d, generator=g).to(torch.bfloat16).to(cuda)
+    q = torch.randn(b * t, h, d, generator=g).to(torch.bfloat16).to(cuda)
+    lengths = torch.randint(750, 2401, (b,), generator=g).to(cuda)
+    kernels.draft_attention(q, kc, vc, lengths, t, cap, d ** -0.5)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        graph.capture_begin()
+        out = kernels.draft_attention(q, kc, vc, lengths, t, cap, d ** -0.5)
+        graph.capture_end()
+    torch.cuda.current_stream().wait_stream(s)
+    gd = torch.Generator(device=cuda).manual_seed(9)
+    for rep in range(4):
+        lengths.copy_(torch.randint(0, cap - t, (b,), device=cuda, generator=gd))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = kernels.draft_attention(q, kc, vc, lengths, t, cap, d ** -0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), rep
+    assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
+
+
 @pytest.mark.parametrize("split_k", [False, True])
 def test_verify_attention_graph_replays(cuda, split_k):
     """Captured in a HIP graph: every replay equals the eager result bit for bit (both decompositions)."""
