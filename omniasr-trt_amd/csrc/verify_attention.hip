@@ -752,17 +752,25 @@ __device__ __forceinline__ int run_tiles(KVTile<D>& X, KVTile<D>& Y, int n, LD l
 template <int NS>
 __device__ __forceinline__ PartialItem merge_slots(const float* po, const float* pm, const float* pl, int T, int D,
                                                    int t, int d) {
+  // Every read is issued before the first use, so that their LDS latencies overlap.
+  float mv[NS], lv[NS];
+  f32x4_t ov[NS];
+#pragma unroll
+  for (int v = 0; v < NS; ++v) {
+    mv[v] = pm[v * T + t];
+    lv[v] = pl[v * T + t];
+    ov[v] = *reinterpret_cast<const f32x4_t*>(po + (v * T + t) * D + d);
+  }
   float top = -INFINITY;
 #pragma unroll
-  for (int v = 0; v < NS; ++v) top = fmaxf(top, pm[v * T + t]);
+  for (int v = 0; v < NS; ++v) top = fmaxf(top, mv[v]);
   float den = 0.f;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int v = 0; v < NS; ++v) {
-    const float mv = pm[v * T + t];
-    const float wt = mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - top);
-    den += wt * pl[v * T + t];
-    acc += wt * *reinterpret_cast<const f32x4_t*>(po + (v * T + t) * D + d);
+    const float wt = mv[v] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv[v] - top);
+    den += wt * lv[v];
+    acc += wt * ov[v];
   }
   return PartialItem{top, den, acc};
 }
