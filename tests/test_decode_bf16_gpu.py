@@ -4,8 +4,8 @@ greedy loop (oracle, fp64 on the CPU, built from the very same bf16 weights).
 * head dim 128, 16 heads, 8 slots: rows x heads = 128, so every drafted / one-token step's verify attention is the
   halves kernel (``verify_attn_pair_kernel<128>``), inside the graph-captured step, with the bf16 RoPE + append, the
   bf16 argmax + acceptance and the proposal kernel around it;
-* head dim 512, 8 heads (the real checkpoint's attention shape): split-K on the wide-head slice kernel and its merge
-  launch.
+* head dim 512, 8 heads (the real checkpoint's attention shape): the wide-head slice kernel in its balanced form
+  (a fixed number of workgroups per head dealt to the rows by length, the splits merged in the kernel).
 
 bf16 activations round differently from fp64, so a step whose two best tokens are within that error may go either
 way, and both are correct roundings of the same search.  The fixtures are contexts whose oracle run has no such step:
