@@ -205,9 +205,12 @@ __device__ __forceinline__ f32x4_t get_through4(const float* base, int64_t at) {
 #endif
 }
 
+// The partials of (row b, head h) merged by one wave, each read at the coherence point: the row's ``nact`` key
+// splits from slot ``first_slot`` on (default: the unit's own slots), then the generated keys' partial if any (slot
+// ``gen_slot``; default: gen_split past the unit's first slot).
 template <typename OutT>
 __device__ void merge_splits_fast(const AttnArgs& a, int b, int h, int nact, int d0 = 0, int dw = -1,
-                                  int64_t first_slot = -1) {
+                                  int64_t first_slot = -1, int64_t gen_slot = -1) {
   constexpr int kS = 8, kR = 3;
   const int lane = lane_id();
   const int T = a.T, D = a.D;
@@ -215,6 +218,7 @@ __device__ void merge_splits_fast(const AttnArgs& a, int b, int h, int nact, int
   const int nf = T * dw;
   const int nq = nact + (a.gen_split >= 0 ? 1 : 0);
   const int64_t split0 = first_slot >= 0 ? first_slot : ((int64_t)b * a.H + h) * a.splits;
+  const int64_t gslot = gen_slot >= 0 ? gen_slot : split0 + a.gen_split;
   OutT* out = reinterpret_cast<OutT*>(a.out);
   for (int f0 = 0; f0 < nf; f0 += kR * 256) {
     float top[kR], den[kR];
@@ -238,7 +242,7 @@ __device__ void merge_splits_fast(const AttnArgs& a, int b, int h, int nact, int
           ov[sq][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
           if (q0 + sq < nq && f < nf) {
             const int t = f / dw;
-            const int64_t slot = (split0 + merge_slot(a, nact, q0 + sq)) * T + t;
+            const int64_t slot = (q0 + sq < nact ? split0 + q0 + sq : gslot) * T + t;
             const uint64_t ml = __hip_atomic_load(reinterpret_cast<uint64_t*>(a.part_ml + slot * 2), __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT);
             mv[sq][r] = __uint_as_float((uint32_t)ml);
@@ -673,7 +677,10 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
   if (threadIdx.x == 0) s_ticket = __hip_atomic_fetch_add(counter, 1, kTicketOrder, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   if (s_ticket != r.nact - 1) return;
-  merge_splits_fast<uint16_t>(a, b, h, r.nact, sl * 128, 128, slot0);  // the last split merges; each wave its slice
+  // The last split merges; each wave its slice.  Balanced beams: the generated keys' partials follow the heads'
+  // workgroup slots, one per (group, head).
+  const int64_t gen_slot = a.balanced ? (int64_t)a.H * a.splits + (int64_t)b * a.H + h : -1;
+  merge_splits_fast<uint16_t>(a, b, h, r.nact, sl * 128, 128, slot0, gen_slot);
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -1319,6 +1326,27 @@ static bool balanced_shape(int32_t rows, int32_t heads, int32_t head_dim) {
   return (head_dim == 256 || head_dim == 512) && rows <= kBalancedMaxRows && balanced_budget(rows, heads) <= 65535;
 }
 
+// The balanced wide-head launch (bf16, head dim 256 / 512, balanced_shape): grid (budget, heads), every key of a row
+// in its one range (the deal splits it), the partials merged in the kernel -- with the generated keys' partial when
+// a.gen_split >= 0 (beams; see verify_attn_slice_kernel).  a.T > 16 runs two query groups per wave.
+static void launch_balanced_wide(AttnArgs& a, int32_t rows, int32_t heads, int32_t head_dim, int32_t keys,
+                                 hipStream_t s) {
+  a.balanced = 1;
+  a.rows = rows;
+  a.splits = balanced_budget(rows, heads);
+  a.ctx_splits = 1;
+  a.chunk = (keys + 31) / 32 * 32;
+  a.separate = 0;
+  dim3 grid(a.splits, heads, 1);
+  if (head_dim == 256) {
+    if (a.T > 16) verify_attn_slice_kernel<256, 2><<<grid, 128, 0, s>>>(a);
+    else verify_attn_slice_kernel<256, 1><<<grid, 128, 0, s>>>(a);
+  } else {
+    if (a.T > 16) verify_attn_slice_kernel<512, 2><<<grid, 256, 0, s>>>(a);
+    else verify_attn_slice_kernel<512, 1><<<grid, 256, 0, s>>>(a);
+  }
+}
+
 // Partial items (T x D floats and their (m, l)) the workspace holds: split-K slots per (row, head) -- a unit's splits
 // or its two halves -- or, for the balanced wide-head split-K, the heads' workgroup slots.
 static size_t attn_partial_items(int32_t rows, int32_t tokens, int32_t heads, int32_t head_dim, int32_t keys,
@@ -1469,19 +1497,7 @@ extern "C" int omni_verify_attention(const void* q, const void* k_cache, const v
   if (dtype == OMNI_BF16 && stride_pos == head_dim && balanced_shape(rows, heads, head_dim) &&
       !(flags & OMNI_ATTN_SPLIT_K)) {
     // wide heads: a fixed budget of workgroups per head dealt to the rows by length, merged in the kernel
-    a.balanced = 1;
-    a.splits = balanced_budget(rows, heads);
-    a.ctx_splits = 1;
-    a.chunk = (keys + 31) / 32 * 32;  // every key of a row is in its (one) range; the deal splits it
-    a.separate = 0;
-    dim3 grid(a.splits, heads, 1);
-    if (head_dim == 256) {
-      if (tokens > 16) verify_attn_slice_kernel<256, 2><<<grid, 128, 0, s>>>(a);
-      else verify_attn_slice_kernel<256, 1><<<grid, 128, 0, s>>>(a);
-    } else {
-      if (tokens > 16) verify_attn_slice_kernel<512, 2><<<grid, 256, 0, s>>>(a);
-      else verify_attn_slice_kernel<512, 1><<<grid, 256, 0, s>>>(a);
-    }
+    launch_balanced_wide(a, rows, heads, head_dim, keys, s);
     return omni_launch_status();
   }
   st = launch_attention(a, rows, dtype, s);
@@ -1887,7 +1903,11 @@ extern "C" size_t omni_beam_attention_workspace(int32_t groups, int32_t beams, i
   if (chunk <= 0) chunk = omni_verify_attention_chunk(groups, beams, heads, head_dim, ctx_keys);
   size_t splits = (size_t)attn_splits(ctx_keys, chunk) + 1;
   if (splits < 3) splits = 3;  // or the two context halves and the generated keys
-  const size_t units = (size_t)groups * heads * splits * beams;
+  size_t units = (size_t)groups * heads * splits * beams;
+  if (balanced_shape(groups, heads, head_dim)) {  // the heads' workgroup slots, then one generated-keys slot per unit
+    const size_t wide = ((size_t)heads * balanced_budget(groups, heads) + (size_t)groups * heads) * beams;
+    units = units > wide ? units : wide;
+  }
   return align256(units * head_dim * sizeof(float)) + align256(units * 2 * sizeof(float));
 }
 
@@ -1918,7 +1938,11 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
   if (!attention_aligned(q, out, k_ctx, v_ctx, ctx_row, ctx_head, ctx_pos, head_dim, dtype)) return OMNI_ERR_INVALID;
   const int ctx_splits = attn_splits(ctx_keys, chunk);
   const int splits = ctx_splits + 1 > 3 ? ctx_splits + 1 : 3;  // partial slots per unit (see the workspace)
-  const size_t units = (size_t)groups * heads * splits * beams;
+  size_t units = (size_t)groups * heads * splits * beams;
+  if (balanced_shape(groups, heads, head_dim)) {  // the workspace's layout (see omni_beam_attention_workspace)
+    const size_t wide = ((size_t)heads * balanced_budget(groups, heads) + (size_t)groups * heads) * beams;
+    units = units > wide ? units : wide;
+  }
   AttnArgs a;
   a.q = q;
   a.k = k_ctx;
@@ -1948,12 +1972,21 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
   const bool halves = dtype == OMNI_BF16 && head_dim == 128 && ctx_pos == head_dim && beams <= kWgMaxT &&
                       groups <= kPairMaxRows && counters != nullptr && (int64_t)groups * heads >= kWgMinUnits &&
                       (int64_t)groups * beams * heads < kPairMaxQueryRows;
+  const bool balanced = !halves && dtype == OMNI_BF16 && ctx_pos == head_dim && counters != nullptr &&
+                        balanced_shape(groups, heads, head_dim);
+  int gen_splits = splits, gen_slot = ctx_splits;  // where the generated keys' kernel writes: unit slot gen_slot
   if (halves) {  // the generated keys' partial first, then the context halves, whose last merge includes it
     a.chunk = (ctx_keys + 31) / 32 * 32;
     a.ctx_splits = 1;
     a.gen_split = 2;
     a.splits = splits;  // >= 3 slots per unit (see omni_beam_attention_workspace)
     a.counters = counters;
+    gen_slot = 2;
+  } else if (balanced) {  // the same order: the generated keys first, then the balanced context launch merging it
+    a.counters = counters;
+    a.gen_split = 0;  // present; its slot is given by the kernel's balanced layout
+    gen_splits = 1;
+    gen_slot = heads * balanced_budget(groups, heads);  // slot heads x budget + (group x heads + head)
   } else {
     st = launch_attention(a, groups, dtype, s);
     if (st != OMNI_OK) return st;
@@ -1977,8 +2010,8 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
   gargs.part_o = a.part_o;
   gargs.part_ml = a.part_ml;
   dim3 ggrid(heads, groups * beams);
-  gargs.splits = a.splits;
-  gargs.gen_split = a.gen_split;
+  gargs.splits = gen_splits;
+  gargs.gen_split = gen_slot;
   if (dtype == OMNI_BF16 && head_dim == 128 && gen_pos == head_dim) beam_gen_kernel_d128<<<ggrid, 64, 0, s>>>(gargs);
   else if (dtype == OMNI_BF16 && head_dim == 512 && gen_pos == head_dim) beam_gen_kernel_d512<<<ggrid, 256, 0, s>>>(gargs);
   else if (dtype == OMNI_BF16) beam_gen_kernel<uint16_t><<<ggrid, 64, 0, s>>>(gargs);
@@ -1988,6 +2021,10 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
   if (halves) {
     verify_attn_pair_kernel<128><<<groups * heads, 64 * kWgWaves, pair_lds_bytes(beams, head_dim), s>>>(a, groups,
                                                                                                          a.splits);
+    return omni_launch_status();
+  }
+  if (balanced) {
+    launch_balanced_wide(a, groups, heads, head_dim, ctx_keys, s);
     return omni_launch_status();
   }
   return launch_combine(a, groups, dtype, s);

@@ -98,6 +98,47 @@ def test_beam_attention_context_halves(cuda, beams):
     _beam_case(cuda, torch.bfloat16, 8, beams, 32, 128, keys, 96, ctx_len, gen_len, keys, 71, BF16_TOL)
 
 
+@pytest.mark.parametrize("beams", [1, 5, 16])
+def test_beam_attention_wide_balanced(cuda, beams):
+    """8 inputs x 8 heads x 512 (the real checkpoint's shape): the context by the balanced wide-head kernel, whose
+    last workgroup of each (input, head) merges the context splits with the generated keys' partial -- finished
+    inputs (no context, no generated keys), a context shorter than a tile, generated keys only, up to 16 beams."""
+    g = torch.Generator().manual_seed(90 + beams)
+    ctx_len = torch.tensor([2300, 0, 17, 1500, 0, 640, 999, 33])
+    gen_len = torch.randint(0, 97, (8 * beams,), generator=g)
+    gen_len[beams: 2 * beams] = 0  # input 1 finished
+    out = _beam_case(cuda, torch.bfloat16, 8, beams, 8, 512, 2304, 96, ctx_len, gen_len, 2304, 91, BF16_TOL)
+    assert torch.all(out[beams: 2 * beams] == 0)
+
+
+def test_beam_attention_wide_graph_replays(cuda):
+    """The balanced wide-head path (4 inputs x 3 beams x 8 heads x 512) captured once and replayed with new lengths
+    and pointers; every replay equals the eager call bit for bit (the tickets are left zero between calls)."""
+    q, kc, vc, kg, vg, ptr, cl, gl = _beam_inputs(torch.bfloat16, 4, 3, 8, 512, 1024, 64, [1000, 0, 77, 1024],
+                                                  [5, 0, 17, 64, 33, 1, 9, 3, 60, 2, 0, 41], 14)
+    q, kc, vc, kg, vg, ptr, cl, gl = (t.to(cuda) for t in (q, kc, vc, kg, vg, ptr, cl, gl))
+    kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr, gl, 3, 1024, 512 ** -0.5)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        graph.capture_begin()
+        out = kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr, gl, 3, 1024, 512 ** -0.5)
+        graph.capture_end()
+    torch.cuda.current_stream().wait_stream(stream)
+    g = torch.Generator(device=cuda).manual_seed(4)
+    for rep in range(4):
+        ptr.copy_(torch.randint(0, 14, ptr.shape, device=cuda, generator=g, dtype=torch.int32))
+        gl.copy_(torch.randint(0, 65, gl.shape, device=cuda, generator=g))
+        cl.copy_(torch.randint(0, 1025, cl.shape, device=cuda, generator=g))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr, gl, 3, 1024, 512 ** -0.5)
+        assert torch.equal(out, eager), rep
+
+
 def test_beam_attention_graph_replays(cuda):
     """Captured once, replayed with new pointers and lengths written in place between replays."""
     q, kc, vc, kg, vg, ptr, cl, gl = _beam_inputs(torch.bfloat16, 4, 3, 8, 128, 512, 128, [500, 200, 37, 512],

@@ -48,6 +48,14 @@ def test_workspace_and_split_queries():
             units = max(units, h * max(rows, 256 // h) * t)
         want = -(-units * d * 4 // 256) * 256 + -(-units * 2 * 4 // 256) * 256
         assert lib.omni_verify_attention_workspace(rows, t, h, d, keys, 0) == want
+    for groups, beams, h, d, keys in ((8, 5, 32, 128, 2560), (8, 5, 8, 512, 2304), (4, 16, 8, 256, 1024),
+                                      (65, 2, 8, 512, 512)):
+        chunk = lib.omni_verify_attention_chunk(groups, beams, h, d, keys)
+        units = groups * h * max(-(-keys // chunk) + 1, 3) * beams  # key splits (or two halves) + generated keys
+        if d in (256, 512) and groups <= 64:  # balanced: the heads' workgroup slots, one generated-keys slot per unit
+            units = max(units, (h * max(groups, 256 // h) + groups * h) * beams)
+        want = -(-units * d * 4 // 256) * 256 + -(-units * 2 * 4 // 256) * 256
+        assert lib.omni_beam_attention_workspace(groups, beams, h, d, keys, 0) == want
     # config 3: 8 rows x 32 heads, keys 2560 -> 320 keys for 2048 waves, capped at 8 tiles per split
     assert lib.omni_verify_attention_chunk(8, 5, 32, 128, 2560) == 256
     # the real model's 8 heads x 512: whole-tile waves, 256 keys per split (measured fastest on MI355X)
