@@ -160,8 +160,9 @@ size_t omni_beam_attention_workspace(int32_t groups, int32_t beams, int32_t head
  * key at all gives zeros.  One pass over a group's context serves all of its beams (the kernels of
  * omni_verify_attention with every query over the same keys); the generated keys are read by a
  * pointer-chasing kernel into one more partial.  bf16, head_dim 128, contiguous key rows, beams <= 11 and
- * groups * heads >= 128: the context halves kernel merges that partial in its last step (``counters``:
- * groups*heads int32 tickets, zero before the first call, left zero); otherwise split-K and a merge launch.
+ * groups * heads >= 128: the context halves kernel merges that partial in its last step; bf16, head_dim 256 /
+ * 512, contiguous key rows, groups <= 64: the balanced wide-head kernel does (``counters``: groups*heads int32
+ * tickets, zero before the first call, left zero); otherwise split-K and a merge launch.
  * ``chunk``: context keys per split (0: the library's choice).  ``workspace``: at least
  * omni_beam_attention_workspace() bytes, 256-byte aligned.  beams: 1..16.
  */
