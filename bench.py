@@ -562,8 +562,8 @@ def main() -> int:
                    "positions at 32 x 128 and at the real checkpoint's 8 x 512 (for counter runs)")
     args = p.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: every box has one MI355X and the step shards by slot with no exchange "
-              f"(DESIGN.md); --gpus {args.gpus} is not run.", file=sys.stderr)
+        print(f"bench.py measures one GPU: every box has one MI355X, and the step shards by slot with no exchange "
+              f"(each GPU runs the same kernels on its own slots); --gpus {args.gpus} is not run.", file=sys.stderr)
         return 2
     import torch
 
