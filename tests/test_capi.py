@@ -101,6 +101,27 @@ def test_argument_errors_before_launch():
     assert lib.omni_greedy_accept(*g) == -2
 
 
+def test_workspaces_past_4_gib_are_refused_before_launch():
+    """The partials are addressed with 32-bit offsets (16-byte buffer stores): a shape whose workspace reaches 4 GiB is
+    refused with OMNI_ERR_SHAPE, before the workspace size or any pointer is looked at."""
+    lib = _lib.load()
+    rows, t, h, d, keys, chunk = 256, 16, 64, 128, 8192, 256
+    assert lib.omni_verify_attention_workspace(rows, t, h, d, keys, chunk) >= 1 << 32
+    args = [FAKE, FAKE, FAKE, 1 << 30, 1 << 20, 128, 8192, FAKE, rows, t, h, d, keys, chunk, 0.1, FAKE, FAKE, 1 << 40,
+            FAKE, 0, _lib.BF16, None]
+    assert lib.omni_verify_attention(*args) == -3
+    args[8] = 8  # the same call at 8 rows fits: the missing workspace is what it then refuses
+    args[17] = 16
+    assert lib.omni_verify_attention(*args) == -4
+    groups, beams, h, d, keys = 64, 16, 64, 512, 8192
+    assert lib.omni_beam_attention_workspace(groups, beams, h, d, keys, 32) >= 1 << 32
+    beam = [FAKE, FAKE, FAKE, 1 << 30, 1 << 24, 512, 8192, FAKE, FAKE, FAKE, 1 << 30, 1 << 24, 512, 64, 1024, FAKE, 64,
+            FAKE, groups, beams, h, d, keys, 32, 0.1, FAKE, FAKE, 1 << 40, FAKE, _lib.BF16, None]
+    assert lib.omni_beam_attention(*beam) == -3
+    beam[18], beam[27] = 2, 16  # 2 groups fit: the missing workspace is what it then refuses
+    assert lib.omni_beam_attention(*beam) == -4
+
+
 def test_kernels_refuse_without_gpu():
     import torch
 
