@@ -134,7 +134,8 @@ int omni_verify_attention(const void *q, const void *k_cache, const void *v_cach
  * OMNI_STATIC_WORKSPACE_BYTES, or with rows * heads > OMNI_STATIC_MAX_UNITS, returns OMNI_ERR_WORKSPACE
  * before anything is launched.  Each call first clears the tickets with a fill kernel on ``stream``, then
  * launches what omni_verify_attention launches.  Every call on a GPU shares that GPU's array: calls that
- * overlap in time on one GPU (other streams, other threads) race and must not be made.
+ * overlap in time on one GPU (other streams, other threads) race and must not be made.  The array used is the
+ * current device's (hipGetDevice), so ``stream`` must belong to the current device, as the caller's buffers do.
  */
 int omni_verify_attention_static(const void *q, const void *k_cache, const void *v_cache,
                                  int64_t stride_row, int64_t stride_head, int64_t stride_pos,
