@@ -273,6 +273,41 @@ int omni_greedy_accept(const void *logits, int64_t logits_stride, int32_t vocab,
                        const uint8_t *use_draft, int32_t rows, int32_t tokens_per_row,
                        int64_t limit, int64_t eos, void *stream);
 
+/*
+ * The beam step's bookkeeping before its layers.  Replaces the torch ops of ``BeamDecoder.step_beam``
+ * before the layers (src/omniasr_trt/beam.py:127-145: live rows, positions, key counts, the row's own
+ * pointer at the position it writes).
+ *
+ * Rows r = g*beams + i of groups g < groups: live = !group_done[g], k = k_step[g];
+ * pos[r] = ctx[g] + k - 1, gen_pos[r] = max(k - 1, 0), gen_len[r] = live ? k : 0,
+ * ctx_len[g] = group_done[g] ? 0 : ctx[g], and for live rows ptr[r*ptr_stride + gen_pos[r]] = r (rows whose
+ * gen_pos is not below ptr_cols are left alone).  beams: 1..16.
+ */
+int omni_beam_prepare(int32_t groups, int32_t beams, const int64_t *ctx, const int64_t *k_step,
+                      const uint8_t *group_done, int32_t *ptr, int64_t ptr_stride, int64_t ptr_cols,
+                      int64_t *pos, int64_t *gen_pos, int64_t *ctx_len, int64_t *gen_len, void *stream);
+
+/*
+ * The beam step's bookkeeping after the per-group top-``beams`` of the offers.  Replaces the torch ops
+ * of ``BeamDecoder.step_beam`` after the top-k and the parent reorder (src/omniasr_trt/beam.py:159-187).
+ *
+ * ``best`` / ``flat``: torch.topk(offers.view(groups, beams * vocab), beams) values (fp32 or fp64, as the
+ * row scores: ``score_bytes`` 4 or 8) and indices.  Row r = g*beams + i, live = !group_done[g],
+ * k = k_step[g]: parent = live ? g*beams + flat[r] / vocab : r, chosen = live ? flat[r] % vocab : tok[r],
+ * EOS when ended[parent]; row r's ptr and hist rows (``ptr_cols`` / ``hist_cols`` columns) become the
+ * parent's, and a live row's hist[r][k] = chosen; extends = live && !ended[parent]: score[r] = extends ?
+ * best[r] : score[parent], count[r] = count[parent] + (extends && chosen != pad && chosen != eos),
+ * ended[r] = live ? chosen == eos : ended[parent], tok[r] = chosen.  Then k_step[g] += live and
+ * group_done[g] |= all rows of g ended || ctx[g] + k_step[g] - 2 >= limit.  Values are moved, never
+ * recomputed, so the state equals the torch ops' bit for bit.  beams: 1..16.
+ */
+int omni_beam_take_over(int32_t groups, int32_t beams, int64_t vocab, const void *best, const int64_t *flat,
+                        int32_t *ptr, int64_t ptr_stride, int64_t ptr_cols, int32_t *hist,
+                        int64_t hist_stride, int64_t hist_cols, uint8_t *ended, void *score,
+                        int32_t score_bytes, int64_t *count, int64_t *tok, int64_t *k_step,
+                        uint8_t *group_done, const int64_t *ctx, int64_t limit, int32_t eos, int32_t pad,
+                        void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,9 @@ _SIGNATURES = {
                             c_int64, _P]),
     "omni_greedy_accept": (c_int, [_P, c_int64, c_int32, c_int32, _P, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P,
                                    _P, c_int32, c_int32, c_int64, c_int64, _P]),
+    "omni_beam_prepare": (c_int, [c_int32, c_int32, _P, _P, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P]),
+    "omni_beam_take_over": (c_int, [c_int32, c_int32, c_int64, _P, _P, _P, c_int64, c_int64, _P, c_int64, c_int64,
+                                    _P, _P, c_int32, _P, _P, _P, _P, _P, c_int64, c_int32, c_int32, _P]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -65,11 +65,16 @@ class BeamDecoder(GreedyDecoder):
         self.score = torch.zeros(rows, dtype=torch.promote_types(torch.float32, self.dtype), device=dev)
         self.ended = torch.ones(rows, dtype=torch.bool, device=dev)
         self.count = torch.zeros(rows, dtype=torch.long, device=dev)  # tokens other than PAD / EOS (length_norm)
-        self.row_ids = torch.arange(rows, device=dev)
         # Group state: tokens chosen in the current context, the context's length, finished.
         self.k_step = torch.zeros(max_batch, dtype=torch.long, device=dev)
         self.ctx = torch.ones(max_batch, dtype=torch.long, device=dev)
         self.gdone = torch.ones(max_batch, dtype=torch.bool, device=dev)
+        # A step's inputs, rewritten by every step before its layers: rows' input and generated-cache positions,
+        # the groups' context key counts, the rows' generated key counts.
+        self.row_pos = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.gen_pos = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.ctx_len = torch.zeros(max_batch, dtype=torch.long, device=dev)
+        self.gen_len = torch.zeros(rows, dtype=torch.long, device=dev)
         self.kc = self.vc = self.kg = self.vg = self.ptr = self.hist = None
         self.ccap = self.gcap = 0
         self._normal_caps: tuple[int, int] | None = None
@@ -129,24 +134,16 @@ class BeamDecoder(GreedyDecoder):
         return offers
 
     def step_beam(self, s: int, ckeys: int) -> None:
-        """One step of groups 0..s-1 (rows 0..s*N-1), in place; finished groups keep their state.
-        (src/omniasr_trt/beam.py:127-187)"""
+        """One step of groups 0..s-1 (rows 0..s*N-1), in place; finished groups keep their state.  The bookkeeping
+        before the layers and after the top-k runs in one launch each (``kernels.beam_prepare`` /
+        ``kernels.beam_take_over``).  (src/omniasr_trt/beam.py:127-187)"""
         n, r = self.beams, s * self.beams
-        group_done = self.gdone[:s]
-        live = ~group_done.repeat_interleave(n)  # [R]
-        k = self.k_step[:s].repeat_interleave(n)  # the token in ``tok`` is hist[row, k - 1]
-        rows = self.row_ids[:r]
-        tok, ptr, hist = self.tok[:r], self.ptr[:r], self.hist[:r]
-        pos = self.ctx[:s].repeat_interleave(n) + k - 1  # input position of ``tok``
-        gen_pos = (k - 1).clamp(min=0)  # its generated cache position
-        ctx_len = self.ctx[:s].masked_fill(group_done, 0)
-        gen_len = k.masked_fill(~live, 0)
-        # A live row writes generated position gen_pos in this step, and this step's attention reads it already:
-        # its pointer there names the row itself.
-        here = gen_pos[:, None]
-        ptr.scatter_(1, here, torch.where(live[:, None], rows[:, None].to(ptr.dtype), ptr.gather(1, here)))
+        ptr = self.ptr[:r]
+        kernels.beam_prepare(s, n, self.ctx, self.k_step, self.gdone, ptr, self.row_pos, self.gen_pos, self.ctx_len,
+                             self.gen_len)
+        pos, gen_pos, ctx_len, gen_len = self.row_pos[:r], self.gen_pos[:r], self.ctx_len[:s], self.gen_len[:r]
         scale = self.head_dim ** -0.5
-        h = self.m.text_frontend.weight[tok]
+        h = self.m.text_frontend.weight[self.tok[:r]]
         for i in range(len(self.layers)):
             kg, vg = self.kg[i], self.vg[i]
 
@@ -159,32 +156,8 @@ class BeamDecoder(GreedyDecoder):
         logp = F.log_softmax(self._head(h), dim=-1)  # [R, V], model dtype
         vocab = logp.size(-1)
         best, flat = self._offers(logp, r).view(s, n * vocab).topk(n, dim=-1, sorted=True)  # [S, N], best first
-        lead = (torch.arange(s, device=self.device) * n)[:, None]
-        parent = torch.where(live, (flat // vocab + lead).view(-1), rows)
-        chosen = torch.where(live, (flat % vocab).view(-1), tok)
-        self._take_over(parent, chosen, best.view(-1), live, k, r)
-        self.k_step[:s] += (~group_done).long()
-        ended_groups = self.ended[:r].view(s, n).all(-1)
-        group_done |= ended_groups | (self.ctx[:s] + self.k_step[:s] - 2 >= LIMIT)
-
-    def _take_over(self, parent: Tensor, chosen: Tensor, best: Tensor, live: Tensor, k: Tensor, r: int) -> None:
-        """Each row r becomes a copy of ``parent[r]`` (history, pointers, score, count, finished) extended by
-        ``chosen[r]`` (EOS when the parent had finished) at step k; live rows whose parent was still open take the
-        offer ``best[r]`` as their score."""
-        ptr, hist = self.ptr[:r], self.hist[:r]
-        ptr.copy_(ptr.index_select(0, parent))
-        hist.copy_(hist.index_select(0, parent))
-        was_ended = self.ended[:r].index_select(0, parent)
-        was_score = self.score[:r].index_select(0, parent)
-        was_count = self.count[:r].index_select(0, parent)
-        chosen = chosen.masked_fill(was_ended, EOS)
-        col = k[:, None]
-        hist.scatter_(1, col, torch.where(live[:, None], chosen[:, None].to(hist.dtype), hist.gather(1, col)))
-        extends = live & ~was_ended
-        self.score[:r] = torch.where(extends, best, was_score)
-        self.count[:r] = was_count + (extends & (chosen != PAD) & (chosen != EOS)).long()
-        self.ended[:r] = torch.where(live, chosen == EOS, was_ended)
-        self.tok[:r] = chosen
+        kernels.beam_take_over(best, flat, vocab, ptr, self.hist[:r], self.ended, self.score, self.count, self.tok,
+                               self.k_step, self.gdone, self.ctx, LIMIT, EOS, PAD)
 
     def beam_runner(self, s: int, ckeys: int):
         """The step of groups 0..s-1 with ``ckeys`` context positions in reach, as a callable (a graph replay per

@@ -411,3 +411,61 @@ def greedy_accept(logits: torch.Tensor, tokens: torch.Tensor, out: torch.Tensor,
                                     _stream(logits))
     _lib.check(status, "greedy_accept")
     return nxt
+
+
+def _flags(t: torch.Tensor, name: str) -> None:
+    _need(t.dtype == torch.bool and t.is_contiguous() and t.is_cuda, f"{name}: contiguous bool on the GPU")
+
+
+def beam_prepare(groups: int, beams: int, ctx: torch.Tensor, k_step: torch.Tensor, group_done: torch.Tensor,
+                 ptr: torch.Tensor, pos: torch.Tensor, gen_pos: torch.Tensor, ctx_len: torch.Tensor,
+                 gen_len: torch.Tensor) -> None:
+    """The beam step's bookkeeping before its layers, in one launch (src/omniasr_trt/beam.py:127-145): for the rows
+    of groups 0..groups-1, ``pos`` = ctx + k - 1, ``gen_pos`` = max(k - 1, 0), ``gen_len`` = k (0 in a finished
+    group), ``ctx_len`` = ctx (0 when finished), and a live row's ``ptr[r, gen_pos]`` = r.  ``ctx`` / ``k_step`` /
+    ``group_done`` [>=groups]; ``ptr`` [>=rows, G] int32; the outputs [>=rows] / [>=groups] int64."""
+    lib = _lib.load()
+    for name, t in (("ctx", ctx), ("k_step", k_step), ("pos", pos), ("gen_pos", gen_pos), ("ctx_len", ctx_len),
+                    ("gen_len", gen_len)):
+        _index(t, name)
+    _flags(group_done, "group_done")
+    rows = groups * beams
+    _need(ptr.dtype == torch.int32 and ptr.dim() == 2 and ptr.stride(1) == 1 and ptr.size(0) >= rows,
+          "ptr: [>=rows, G] int32")
+    _need(min(ctx.numel(), k_step.numel(), group_done.numel(), ctx_len.numel()) >= groups
+          and min(pos.numel(), gen_pos.numel(), gen_len.numel()) >= rows, "state sizes")
+    status = lib.omni_beam_prepare(groups, beams, ctx.data_ptr(), k_step.data_ptr(), group_done.data_ptr(),
+                                   ptr.data_ptr(), ptr.stride(0), ptr.size(1), pos.data_ptr(), gen_pos.data_ptr(),
+                                   ctx_len.data_ptr(), gen_len.data_ptr(), _stream(ptr))
+    _lib.check(status, "beam_prepare")
+
+
+def beam_take_over(best: torch.Tensor, flat: torch.Tensor, vocab: int, ptr: torch.Tensor, hist: torch.Tensor,
+                   ended: torch.Tensor, score: torch.Tensor, count: torch.Tensor, tok: torch.Tensor,
+                   k_step: torch.Tensor, group_done: torch.Tensor, ctx: torch.Tensor, limit: int, eos: int,
+                   pad: int) -> None:
+    """The beam step's bookkeeping after the top-k (src/omniasr_trt/beam.py:159-187), in one launch: ``best`` /
+    ``flat`` [S, N] are ``offers.view(S, N * vocab).topk(N)``'s values and indices; every row of groups 0..S-1 takes
+    over its parent's ``ptr`` / ``hist`` rows, score, count and finished flag, extended by its chosen token; then
+    the groups' ``k_step`` and ``group_done``.  In place; equal to the torch ops bit for bit."""
+    lib = _lib.load()
+    groups, beams = best.shape
+    rows = groups * beams
+    _need(flat.shape == best.shape and flat.dtype == torch.long and flat.is_contiguous(), "flat: [S, N] int64")
+    _need(best.is_contiguous() and best.dtype == score.dtype and score.dtype in (torch.float32, torch.float64)
+          and score.is_contiguous(), "best / score: fp32 or fp64, contiguous, the same type")
+    for name, t in (("count", count), ("tok", tok), ("k_step", k_step), ("ctx", ctx)):
+        _index(t, name)
+    _flags(ended, "ended")
+    _flags(group_done, "group_done")
+    for name, t in (("ptr", ptr), ("hist", hist)):
+        _need(t.dtype == torch.int32 and t.dim() == 2 and t.stride(1) == 1 and t.size(0) >= rows,
+              f"{name}: [>=rows, G] int32")
+    _need(min(ended.numel(), score.numel(), count.numel(), tok.numel()) >= rows
+          and min(k_step.numel(), group_done.numel(), ctx.numel()) >= groups, "state sizes")
+    status = lib.omni_beam_take_over(groups, beams, int(vocab), best.data_ptr(), flat.data_ptr(), ptr.data_ptr(),
+                                     ptr.stride(0), ptr.size(1), hist.data_ptr(), hist.stride(0), hist.size(1),
+                                     ended.data_ptr(), score.data_ptr(), score.element_size(), count.data_ptr(),
+                                     tok.data_ptr(), k_step.data_ptr(), group_done.data_ptr(), ctx.data_ptr(),
+                                     int(limit), int(eos), int(pad), _stream(best))
+    _lib.check(status, "beam_take_over")

@@ -115,6 +115,65 @@ def beam_attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, ctx_len: np.nd
     return out
 
 
+# ---------------------------------------------------------------------------------------------- beam step
+
+def beam_prepare(groups: int, beams: int, ctx, k_step, group_done, ptr):
+    """The beam step before its layers (src/omniasr_trt/beam.py:133-145), row by row: returns (pos, gen_pos, ctx_len,
+    gen_len) and writes a live row's own index at ptr[r, gen_pos[r]] in place.
+    Pinned by: a hand-computed case and the reference's vectorised formulation of the same step
+    (tests/test_oracle.py)."""
+    rows = groups * beams
+    pos = np.zeros(rows, np.int64)
+    gen_pos = np.zeros(rows, np.int64)
+    gen_len = np.zeros(rows, np.int64)
+    ctx_len = np.zeros(groups, np.int64)
+    for g in range(groups):
+        done = bool(group_done[g])
+        ctx_len[g] = 0 if done else ctx[g]
+        for i in range(beams):
+            r = g * beams + i
+            k = int(k_step[g])
+            pos[r] = ctx[g] - 1 + k
+            gen_pos[r] = max(k - 1, 0)
+            gen_len[r] = 0 if done else k
+            if not done and gen_pos[r] < ptr.shape[1]:
+                ptr[r, gen_pos[r]] = r
+    return pos, gen_pos, ctx_len, gen_len
+
+
+def beam_take_over(best, flat, vocab: int, ptr, hist, ended, score, count, tok, k_step, group_done, ctx, limit: int,
+                   eos: int, pad: int) -> None:
+    """The beam step after the per-group top-N (src/omniasr_trt/beam.py:170-187), row by row, in place: each row of a
+    live group takes over its parent's pointers, history, score, token count and finished flag, extended by its
+    chosen token (EOS after a finished parent); then the group's step counter and finished flag.
+    Pinned by: a hand-computed case, invariants (a finished group keeps its state; rows are a permutation of the old
+    ones within their group) and the reference's vectorised formulation (tests/test_oracle.py)."""
+    groups, beams = best.shape
+    old_ptr, old_hist = ptr.copy(), hist.copy()
+    old_ended, old_score, old_count, old_tok = ended.copy(), score.copy(), count.copy(), tok.copy()
+    for g in range(groups):
+        live = not bool(group_done[g])
+        k = int(k_step[g])
+        for i in range(beams):
+            r = g * beams + i
+            p = g * beams + int(flat[g, i]) // vocab if live else r
+            chosen = int(flat[g, i]) % vocab if live else int(old_tok[r])
+            if old_ended[p]:
+                chosen = eos
+            ptr[r] = old_ptr[p]
+            hist[r] = old_hist[p]
+            if live and k < hist.shape[1]:
+                hist[r, k] = chosen
+            extends = live and not old_ended[p]
+            score[r] = best[g, i] if extends else old_score[p]
+            count[r] = old_count[p] + (1 if extends and chosen not in (pad, eos) else 0)
+            ended[r] = (chosen == eos) if live else old_ended[p]
+            tok[r] = chosen
+        k_step[g] = k + (1 if live else 0)
+        rows = slice(g * beams, (g + 1) * beams)
+        group_done[g] = bool(group_done[g]) or bool(np.all(ended[rows])) or ctx[g] - 1 + k_step[g] - 1 >= limit
+
+
 # ---------------------------------------------------------------------------------------------- argmax
 
 def log_softmax_f32(logits: np.ndarray, lse_shift: int = 0) -> np.ndarray:

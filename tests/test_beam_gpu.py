@@ -294,3 +294,47 @@ def test_position_cap(cuda, monkeypatch):
     dec = BeamDecoder(m, beams=3, max_batch=2, sync_every=4, reserve=16)
     assert dec.generate([c.cuda() for c in ctxs]) == ref
     assert [len(r) for r in ref][2:4] == [3, 1]  # contexts ending at the cap: three tokens, and the first only
+
+
+@pytest.mark.parametrize("beams,score_dtype", [(1, np.float32), (5, np.float32), (16, np.float32), (3, np.float64)])
+def test_beam_step_bookkeeping_vs_oracle(cuda, beams, score_dtype):
+    """``beam_prepare`` and ``beam_take_over`` against the oracle's row-by-row restatement, bit for bit: random
+    states with finished groups, ended rows and EOS / PAD choices, two spare groups of rows past the launch that must
+    stay untouched, vocabularies up to the config's, ptr / hist rows of 1-300 columns."""
+    from test_oracle import _beam_state
+
+    rng = np.random.default_rng(40 + beams)
+    for trial in range(8):
+        groups, vocab, cols = int(rng.integers(1, 9)), int(rng.integers(3, 10289)), int(rng.integers(2, 301))
+        spare = groups + 2
+        st, best, flat = _beam_state(rng, spare, beams, vocab, cols, score_dtype)
+        best, flat = best[:groups].copy(), flat[:groups].copy()
+        st["k_step"][:] = rng.integers(0, cols, spare)  # includes k = 0 (gen_pos clamps to 0)
+        limit = int(rng.integers(5, 600))
+        say(f"beam bookkeeping: groups={groups} beams={beams} vocab={vocab} cols={cols} score={score_dtype.__name__}")
+        dev = {k: torch.from_numpy(v.copy()).to(cuda) for k, v in st.items()}
+        rows = spare * beams
+        outs = [torch.full((rows,), -7, dtype=torch.long, device=cuda) for _ in range(2)] + \
+               [torch.full((spare,), -7, dtype=torch.long, device=cuda), torch.full((rows,), -7, dtype=torch.long,
+                                                                                  device=cuda)]
+        kernels.beam_prepare(groups, beams, dev["ctx"], dev["k_step"], dev["group_done"], dev["ptr"], *outs)
+        want_ptr = st["ptr"].copy()
+        want = ov.beam_prepare(groups, beams, st["ctx"], st["k_step"], st["group_done"], want_ptr)
+        r = groups * beams
+        np.testing.assert_array_equal(dev["ptr"].cpu().numpy(), want_ptr, err_msg=f"trial {trial}: prepare ptr")
+        for got, w, n in zip(outs, want, (r, r, groups, r)):
+            got = got.cpu().numpy()
+            np.testing.assert_array_equal(got[:n], w, err_msg=f"trial {trial}: prepare")
+            assert (got[n:] == -7).all()
+        # after the top-k
+        dev["k_step"] = torch.from_numpy(st["k_step"].copy()).clamp(min=1).to(cuda)
+        st["k_step"] = np.maximum(st["k_step"], 1)
+        kernels.beam_take_over(torch.from_numpy(best).to(cuda), torch.from_numpy(flat).to(cuda), vocab, dev["ptr"],
+                               dev["hist"], dev["ended"], dev["score"], dev["count"], dev["tok"], dev["k_step"],
+                               dev["group_done"], dev["ctx"], limit, 2, 1)
+        ref = {k: v.copy() for k, v in st.items()}
+        ref["ptr"] = want_ptr
+        ov.beam_take_over(best, flat, vocab, ref["ptr"], ref["hist"], ref["ended"], ref["score"], ref["count"],
+                          ref["tok"], ref["k_step"], ref["group_done"], ref["ctx"], limit, 2, 1)
+        for key in ("ptr", "hist", "ended", "score", "count", "tok", "k_step", "group_done"):
+            np.testing.assert_array_equal(dev[key].cpu().numpy(), ref[key], err_msg=f"trial {trial}: {key}")

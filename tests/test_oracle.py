@@ -472,3 +472,130 @@ def test_beam_search_two_tokens_brute_force():
         assert oref.beam_reference(dec, c, vocab, limit=n) == want
         differs += oref.greedy_reference(dec, c, limit=n) != want
     assert differs >= 2  # the search found sequences greedy decoding misses
+
+
+# ---------------------------------------------------------------------------------------------- beam step bookkeeping
+
+def _beam_state(rng, groups, beams, vocab, cols, score_dtype=np.float32):
+    rows = groups * beams
+    st = dict(
+        ctx=rng.integers(1, 500, groups).astype(np.int64),
+        k_step=rng.integers(1, cols, groups).astype(np.int64),
+        group_done=rng.random(groups) < 0.3,
+        ptr=rng.integers(0, rows, (rows, cols)).astype(np.int32),
+        hist=rng.integers(0, vocab, (rows, cols + 1)).astype(np.int32),
+        ended=rng.random(rows) < 0.3,
+        score=(rng.standard_normal(rows) * 3).astype(score_dtype),
+        count=rng.integers(0, 50, rows).astype(np.int64),
+        tok=rng.integers(0, vocab, rows).astype(np.int64),
+    )
+    best = np.sort(rng.standard_normal((groups, beams)).astype(score_dtype), axis=1)[:, ::-1].copy()
+    flat = rng.integers(0, beams * vocab, (groups, beams)).astype(np.int64)
+    flat[:, 0] = flat[:, 0] - flat[:, 0] % vocab + 2  # every group's best: EOS (2)
+    if beams > 1:
+        flat[:, 1] = flat[:, 1] - flat[:, 1] % vocab + 1  # the second: PAD (1)
+    return st, best, flat
+
+
+def _beam_take_over_torch(best, flat, vocab, st, limit, eos, pad):
+    """The reference's vectorised formulation of the step after the top-k (src/omniasr_trt/beam.py:170-187), on
+    CPU tensors: the check the row-by-row oracle is held to."""
+    s, n = best.shape
+    r = s * n
+    t = {k: torch.from_numpy(v.copy()) for k, v in st.items()}
+    best, flat = torch.from_numpy(best.copy()), torch.from_numpy(flat.copy())
+    rows = torch.arange(r)
+    group = rows // n
+    live = ~t["group_done"][group]
+    k = t["k_step"][group]
+    parent = torch.where(live, (flat // vocab + torch.arange(s)[:, None] * n).view(-1), rows)
+    new = torch.where(live, (flat % vocab).view(-1), t["tok"])
+    ptr, hist = t["ptr"], t["hist"]
+    ptr.copy_(ptr[parent])
+    hist.copy_(hist[parent])
+    p_ended, p_score, p_count = t["ended"][parent], t["score"][parent], t["count"][parent]
+    new = torch.where(p_ended, eos, new)
+    hist.scatter_(1, k[:, None], torch.where(live, new, hist.gather(1, k[:, None])[:, 0].long())[:, None]
+                  .to(hist.dtype))
+    t["score"].copy_(torch.where(live & ~p_ended, best.view(-1), p_score))
+    t["count"].copy_(p_count + (live & ~p_ended & (new != pad) & (new != eos)).long())
+    t["ended"].copy_(torch.where(live, new == eos, p_ended))
+    t["tok"].copy_(new)
+    all_ended = t["ended"].view(s, n).all(-1)
+    t["k_step"].copy_(t["k_step"] + (~t["group_done"]).long())
+    t["group_done"] |= all_ended | (t["ctx"] - 1 + t["k_step"] - 1 >= limit)
+    return {k: v.numpy() for k, v in t.items()}
+
+
+def test_beam_take_over_oracle_vs_the_vectorised_step():
+    rng = np.random.default_rng(31)
+    for trial in range(60):
+        groups, beams, vocab, cols = int(rng.integers(1, 9)), int(rng.integers(1, 17)), int(rng.integers(3, 40)), 24
+        dt = np.float64 if trial % 3 == 0 else np.float32
+        st, best, flat = _beam_state(rng, groups, beams, vocab, cols, dt)
+        limit = int(rng.integers(5, 600))
+        want = _beam_take_over_torch(best, flat, vocab, st, limit, 2, 1)
+        got = {k: v.copy() for k, v in st.items()}
+        ov.beam_take_over(best, flat, vocab, got["ptr"], got["hist"], got["ended"], got["score"], got["count"],
+                          got["tok"], got["k_step"], got["group_done"], got["ctx"], limit, 2, 1)
+        for key in want:
+            np.testing.assert_array_equal(got[key], want[key], err_msg=f"trial {trial}: {key}")
+
+
+def test_beam_take_over_known_answer():
+    """Two groups of three beams, vocabulary 10: group 0 live (its row 1 had ended), group 1 finished."""
+    best = np.array([[-1.0, -2.0, -3.0], [-0.5, -0.6, -0.7]], np.float32)
+    flat = np.array([[1 * 10 + 7, 0 * 10 + 2, 2 * 10 + 5], [0, 11, 22]], np.int64)  # (parent, token)
+    ptr = np.arange(6 * 4, dtype=np.int32).reshape(6, 4)
+    hist = np.arange(100, 100 + 6 * 5, dtype=np.int32).reshape(6, 5)
+    ended = np.array([False, True, False, True, False, False])
+    score = np.array([-0.1, -0.2, -0.3, -0.4, -0.5, -0.6], np.float32)
+    count = np.array([3, 4, 5, 6, 7, 8], np.int64)
+    tok = np.array([9, 9, 9, 4, 5, 6], np.int64)
+    k_step = np.array([2, 3], np.int64)
+    group_done = np.array([False, True])
+    ctx = np.array([10, 10], np.int64)
+    ov.beam_take_over(best, flat, 10, ptr, hist, ended, score, count, tok, k_step, group_done, ctx, 8188, 2, 1)
+    # row 0: parent 1 (ended) -> EOS, score and count of the parent, still ended
+    # row 1: parent 0 token 2 = EOS -> ended, count unchanged, score -2.0
+    # row 2: parent 2 token 5 -> score -3.0, count 6
+    np.testing.assert_array_equal(tok[:3], [2, 2, 5])
+    np.testing.assert_array_equal(ended[:3], [True, True, False])
+    np.testing.assert_array_equal(score[:3], np.array([-0.2, -2.0, -3.0], np.float32))
+    np.testing.assert_array_equal(count[:3], [4, 3, 6])
+    np.testing.assert_array_equal(ptr[:3], np.arange(24, dtype=np.int32).reshape(6, 4)[[1, 0, 2]])
+    want_hist = np.arange(100, 130, dtype=np.int32).reshape(6, 5)[[1, 0, 2]].copy()
+    want_hist[:, 2] = [2, 2, 5]
+    np.testing.assert_array_equal(hist[:3], want_hist)
+    assert k_step[0] == 3 and not group_done[0]
+    # group 1 is finished: its rows keep their state; tok becomes EOS where the row had ended
+    np.testing.assert_array_equal(tok[3:], [2, 5, 6])
+    np.testing.assert_array_equal(ptr[3:], np.arange(24, dtype=np.int32).reshape(6, 4)[3:])
+    np.testing.assert_array_equal(score[3:], np.array([-0.4, -0.5, -0.6], np.float32))
+    assert k_step[1] == 3 and group_done[1]
+
+
+def test_beam_prepare_oracle():
+    rng = np.random.default_rng(32)
+    for trial in range(30):
+        groups, beams, cols = int(rng.integers(1, 9)), int(rng.integers(1, 17)), 20
+        ctx = rng.integers(1, 500, groups).astype(np.int64)
+        k_step = rng.integers(0, cols + 3, groups).astype(np.int64)
+        done = rng.random(groups) < 0.3
+        ptr = rng.integers(0, 99, (groups * beams, cols)).astype(np.int32)
+        want_ptr = ptr.copy()
+        got = ov.beam_prepare(groups, beams, ctx, k_step, done, ptr)
+        # the reference's vectorised formulation (src/omniasr_trt/beam.py:133-145)
+        r = groups * beams
+        group = np.arange(r) // beams
+        live = ~done[group]
+        k = k_step[group]
+        j = np.maximum(k - 1, 0)
+        np.testing.assert_array_equal(got[0], ctx[group] - 1 + k)
+        np.testing.assert_array_equal(got[1], j)
+        np.testing.assert_array_equal(got[2], np.where(done, 0, ctx))
+        np.testing.assert_array_equal(got[3], np.where(live, k, 0))
+        for row in range(r):
+            if live[row] and j[row] < cols:
+                want_ptr[row, j[row]] = row
+        np.testing.assert_array_equal(ptr, want_ptr)
