@@ -256,6 +256,19 @@ def test_verify_attention_wide_balanced(cuda, rows, heads, d, t):
     assert torch.equal(a, c)  # the deal and the merge order are fixed: the same bits every call
 
 
+@pytest.mark.parametrize("d,h", [(128, 16), (512, 8)])
+def test_verify_attention_maximum_lengths(cuda, d, h):
+    """Rows at the decoder's position cap (8188 positions, plus the step's 5 queries: 33 tiles past 8000 keys per
+    unit), ragged with empty and one-key rows, on the halves kernel (8 x 16 x 128) and the balanced wide-head kernel
+    (8 x 8 x 512); the tickets are left zero."""
+    lengths = torch.tensor([8188, 8187, 4000, 1, 0, 8100, 7777, 33])
+    t = 5
+    keys = -(-(int(lengths.max()) + t) // 256) * 256
+    _attn_case(cuda, torch.bfloat16, 8, h, d, t, keys, lengths, keys, 90 + d, BF16_TOL)
+    torch.cuda.synchronize()
+    assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
+
+
 def test_verify_attention_wide_graph_replays(cuda):
     """The real checkpoint's shape (8 rows x 8 heads x 512, T = 5) captured once and replayed with new lengths written
     in place: every replay equals the eager call bit for bit, and the tickets are left zero."""
