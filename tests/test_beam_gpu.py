@@ -111,6 +111,19 @@ def test_beam_attention_wide_balanced(cuda, beams):
     assert torch.all(out[beams: 2 * beams] == 0)
 
 
+@pytest.mark.parametrize("d,h", [(128, 32), (512, 8)])
+def test_beam_attention_maximum_lengths(cuda, d, h):
+    """Contexts at the position cap (8188 keys), 5 beams, up to 300 generated keys, a finished input: the halves
+    kernel (8 inputs x 32 heads x 128) and the balanced wide-head kernel (8 x 8 x 512)."""
+    g = torch.Generator().manual_seed(95 + d)
+    ctx_len = torch.tensor([8188, 8000, 1, 0, 4097, 8187, 33, 7000])
+    gen_len = torch.randint(0, 301, (40,), generator=g)
+    gen_len[15:20] = 0  # input 3 finished
+    keys = -(-8188 // 256) * 256
+    out = _beam_case(cuda, torch.bfloat16, 8, 5, h, d, keys, 320, ctx_len, gen_len, keys, 96, BF16_TOL)
+    assert torch.all(out[15:20] == 0)
+
+
 def test_beam_attention_wide_graph_replays(cuda):
     """The balanced wide-head path (4 inputs x 3 beams x 8 heads x 512) captured once and replayed with new lengths
     and pointers; every replay equals the eager call bit for bit (the tickets are left zero between calls)."""
