@@ -308,6 +308,26 @@ int omni_beam_take_over(int32_t groups, int32_t beams, int64_t vocab, const void
                         uint8_t *group_done, const int64_t *ctx, int64_t limit, int32_t eos, int32_t pad,
                         void *stream);
 
+/*
+ * RMS norm of each row: y[r][i] = x[r][i] * rsqrt(sum_j x[r][j]^2 / dim + eps) * weight[i], fp32 arithmetic,
+ * one rounding to bf16 after both products.  Replaces the torch kernel of the decoder layers' RMSNorm
+ * (``F.rms_norm``; the RMSNorm of src/omniasr_trt/modeling.py, run by SpecDecoder.step,
+ * src/omniasr_trt/spec.py:97-106), which the reference leaves to torch; no counterpart among its kernels.
+ * dim: a multiple of 8, at most 8192; strides in elements, multiples of 8.  dtype: OMNI_BF16.
+ */
+int omni_rms_norm(const void *x, int64_t x_stride, const void *weight, void *y, int64_t y_stride,
+                  int32_t rows, int32_t dim, float eps, int32_t dtype, void *stream);
+
+/*
+ * The gated FFN's activation: out[r][i] = inner * bf16(silu(gate)), gate = gate_inner[r][i],
+ * inner = gate_inner[r][ffn + i] (the fused gate|inner projection's halves, src/omniasr_trt/decode.py:34-54),
+ * silu(g) = g / (1 + exp(-g)) in fp32 rounded to bf16, then the product in fp32 rounded to bf16 -- the
+ * rounding of torch's ``inner * F.silu(gate)`` (src/omniasr_trt/spec.py:97-106), which the reference leaves
+ * to torch; no counterpart among its kernels.  ffn: a multiple of 8; strides multiples of 8.  dtype: OMNI_BF16.
+ */
+int omni_silu_mul(const void *gate_inner, int64_t gate_inner_stride, void *out, int64_t out_stride,
+                  int32_t rows, int32_t ffn, int32_t dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -88,7 +88,9 @@ __global__ __launch_bounds__(256) void beam_take_over_kernel(int beams, int64_t 
   int64_t new_count = 0;
   if (tid < n) {
     const int64_t fl = flat[r0 + tid];
-    const int p = live ? (int)(fl / vocab) : tid;  // topk's index into the group's N x V offers
+    // topk's index into the group's N x V offers (clamped into the group: an index past it reads no other group)
+    const int64_t fp = fl / vocab;
+    const int p = live ? (int)(fp < 0 ? 0 : fp >= n ? n - 1 : fp) : tid;
     int64_t ch = live ? fl % vocab : tok[r0 + tid];
     const bool was_ended = ended[r0 + p] != 0;
     if (was_ended) ch = eos;

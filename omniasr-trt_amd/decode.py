@@ -23,7 +23,7 @@ from contextlib import nullcontext
 import numpy as np
 import torch
 import torch.nn.functional as F
-from torch import Tensor
+from torch import Tensor, nn
 from torch.nn.utils.rnn import pad_sequence
 
 from . import kernels
@@ -48,6 +48,23 @@ def fuse_projections(model: DecoderModel):
     """Per layer the four GEMM operands (q|k|v, attention output, gate|inner, FFN output) -- see
     :func:`batching.packed_weights`.  (src/omniasr_trt/decode.py:34-54)"""
     return packed_weights(model)
+
+
+def _norm(norm: nn.Module, h: Tensor) -> Tensor:
+    """A decoder RMSNorm on the residual rows: one HIP launch for bf16 rows on the GPU (``kernels.rms_norm``), the
+    module (torch) otherwise."""
+    if kernels.layer_ops_supported(h):
+        return kernels.rms_norm(h, norm.weight, norm.eps)
+    return norm(h)
+
+
+def _gated(gate_inner: Tensor) -> Tensor:
+    """``inner * silu(gate)`` of the fused gate|inner projection: one HIP launch for bf16 rows on the GPU
+    (``kernels.silu_mul``, torch's rounding), torch's two kernels otherwise."""
+    if kernels.layer_ops_supported(gate_inner):
+        return kernels.silu_mul(gate_inner)
+    gate, inner = gate_inner.chunk(2, -1)
+    return inner * F.silu(gate)
 
 
 def _regrown(old: Tensor | None, shape: tuple, dim: int, fill, dtype, device) -> Tensor:
@@ -137,13 +154,12 @@ class GreedyDecoder:
         output [N, H*Dh] for the layer's q|k|v [N, 3*H*Dh] (it also writes the K/V cache)."""
         w = self.layers[i]
         layer = self.m.llama_decoder.layers[i]
-        o = attend(layer.self_attn_layer_norm(h) @ w.qkv.t())
+        o = attend(_norm(layer.self_attn_layer_norm, h) @ w.qkv.t())
         h.addmm_(o, w.attn_out.t())  # the GEMM adds into the residual in place
-        gate, inner = (layer.ffn_layer_norm(h) @ w.gate_inner.t()).chunk(2, -1)
-        h.addmm_(inner * F.silu(gate), w.ffn_out.t())
+        h.addmm_(_gated(_norm(layer.ffn_layer_norm, h) @ w.gate_inner.t()), w.ffn_out.t())
 
     def _head(self, h: Tensor) -> Tensor:
-        return self.m.final_proj(self.m.llama_decoder.layer_norm(h))
+        return self.m.final_proj(_norm(self.m.llama_decoder.layer_norm, h))
 
     # ------------------------------------------------------------------ prefill
 

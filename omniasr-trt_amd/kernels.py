@@ -469,3 +469,38 @@ def beam_take_over(best: torch.Tensor, flat: torch.Tensor, vocab: int, ptr: torc
                                      tok.data_ptr(), k_step.data_ptr(), group_done.data_ptr(), ctx.data_ptr(),
                                      int(limit), int(eos), int(pad), _stream(best))
     _lib.check(status, "beam_take_over")
+
+
+def layer_ops_supported(x: torch.Tensor) -> bool:
+    """Whether ``rms_norm`` / ``silu_mul`` take this activation: bf16 rows on the GPU."""
+    return x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """``F.rms_norm(x, (D,), weight, eps)`` for bf16 x [N, D] (D <= 8192, a multiple of 8): fp32 arithmetic, one
+    rounding after both products.  The norm of the reference's decoder layers (RMSNorm in
+    src/omniasr_trt/modeling.py, run by SpecDecoder.step, spec.py:97-106)."""
+    lib = _lib.load()
+    _need(layer_ops_supported(x) and x.stride(0) % 8 == 0, "rms_norm: bf16 x [N, D] with unit stride")
+    _need(weight.dtype == x.dtype and weight.is_contiguous() and weight.numel() == x.size(1),
+          "rms_norm: weight [D] in x's dtype")
+    y = torch.empty(x.shape, device=x.device, dtype=x.dtype)
+    status = lib.omni_rms_norm(x.data_ptr(), x.stride(0), weight.data_ptr(), y.data_ptr(), y.stride(0), x.size(0),
+                               x.size(1), float(eps), _lib.BF16, _stream(x))
+    _lib.check(status, "rms_norm")
+    return y
+
+
+def silu_mul(gate_inner: torch.Tensor) -> torch.Tensor:
+    """``inner * F.silu(gate)`` for ``gate, inner = gate_inner.chunk(2, -1)``, bf16 [N, 2F] -> [N, F]: silu(gate)
+    rounded to bf16, then the product, as torch's two kernels round.  The FFN of the reference's decoder layers
+    (spec.py:97-106 over the fused gate|inner projection of decode.py:34-54)."""
+    lib = _lib.load()
+    _need(layer_ops_supported(gate_inner) and gate_inner.size(1) % 16 == 0 and gate_inner.stride(0) % 8 == 0,
+          "silu_mul: bf16 gate_inner [N, 2F] with F a multiple of 8")
+    f = gate_inner.size(1) // 2
+    out = torch.empty(gate_inner.size(0), f, device=gate_inner.device, dtype=gate_inner.dtype)
+    status = lib.omni_silu_mul(gate_inner.data_ptr(), gate_inner.stride(0), out.data_ptr(), out.stride(0),
+                               gate_inner.size(0), f, _lib.BF16, _stream(gate_inner))
+    _lib.check(status, "silu_mul")
+    return out

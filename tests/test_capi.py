@@ -146,3 +146,15 @@ def test_static_scratch_refuses_oversized_shapes_before_launch():
     assert lib.omni_verify_attention_static(*args) == -4
     args[9] = 17  # the shape checks of omni_verify_attention come first
     assert lib.omni_verify_attention_static(*args) == -3
+
+
+def test_layer_op_argument_errors_before_launch():
+    lib = _lib.load()
+    assert lib.omni_rms_norm(FAKE, 4096, FAKE, FAKE, 4096, 40, 4096, 1e-5, _lib.F32, None) == -2
+    assert lib.omni_rms_norm(FAKE, 4096, FAKE, FAKE, 4096, 40, 4100, 1e-5, _lib.BF16, None) == -3  # not 8 | dim
+    assert lib.omni_rms_norm(FAKE, 16384, FAKE, FAKE, 16384, 40, 16384, 1e-5, _lib.BF16, None) == -3  # > 8192
+    assert lib.omni_rms_norm(FAKE, 4000, FAKE, FAKE, 4096, 40, 4096, 1e-5, _lib.BF16, None) == -1  # stride < dim
+    assert lib.omni_rms_norm(None, 4096, None, None, 4096, 0, 4096, 1e-5, _lib.BF16, None) == 0  # nothing to do
+    assert lib.omni_silu_mul(FAKE, 22016, FAKE, 11008, 40, 11008, _lib.F32, None) == -2
+    assert lib.omni_silu_mul(FAKE, 22020, FAKE, 11010, 40, 11010, _lib.BF16, None) == -3
+    assert lib.omni_silu_mul(FAKE, 11008, FAKE, 11008, 40, 11008, _lib.BF16, None) == -1  # stride < 2 * ffn
