@@ -21,12 +21,16 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t* 
   __shared__ float part[kNormThreads / kWave];
   const int tid = threadIdx.x;
   const uint16_t* xr = x + (int64_t)blockIdx.x * x_stride;
-  u32x4_t v[kNormChunks];
+  u32x4_t v[kNormChunks], wv[kNormChunks];  // the weights load with x: one memory round trip, not two
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < kNormChunks; ++c) {
     const int i = (tid + c * kNormThreads) * 8;
     v[c] = i < dim ? *reinterpret_cast<const u32x4_t*>(xr + i) : u32x4_t{0u, 0u, 0u, 0u};
+    wv[c] = i < dim ? *reinterpret_cast<const u32x4_t*>(w + i) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float f = bf16x8_elem(v[c], e);
@@ -45,12 +49,11 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const uint16_t* 
   for (int c = 0; c < kNormChunks; ++c) {
     const int i = (tid + c * kNormThreads) * 8;
     if (i >= dim) continue;
-    const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(w + i);
     u32x4_t o;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      o[q] = pack_bf16x2(bf16x8_elem(v[c], 2 * q) * rstd * bf16x8_elem(wv, 2 * q),
-                         bf16x8_elem(v[c], 2 * q + 1) * rstd * bf16x8_elem(wv, 2 * q + 1));
+      o[q] = pack_bf16x2(bf16x8_elem(v[c], 2 * q) * rstd * bf16x8_elem(wv[c], 2 * q),
+                         bf16x8_elem(v[c], 2 * q + 1) * rstd * bf16x8_elem(wv[c], 2 * q + 1));
     *reinterpret_cast<u32x4_t*>(yr + i) = o;
   }
 }
