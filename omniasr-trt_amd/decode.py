@@ -51,9 +51,9 @@ def fuse_projections(model: DecoderModel):
 
 
 def _norm(norm: nn.Module, h: Tensor) -> Tensor:
-    """A decoder RMSNorm on the residual rows: one HIP launch for bf16 rows on the GPU (``kernels.rms_norm``), the
-    module (torch) otherwise."""
-    if kernels.layer_ops_supported(h):
+    """A decoder RMSNorm on the residual rows: one HIP launch for bf16 rows on the GPU (``kernels.rms_norm``; model
+    widths up to 8192), the module (torch) otherwise."""
+    if kernels.rms_norm_supported(h, norm.weight):
         return kernels.rms_norm(h, norm.weight, norm.eps)
     return norm(h)
 

@@ -472,8 +472,15 @@ def beam_take_over(best: torch.Tensor, flat: torch.Tensor, vocab: int, ptr: torc
 
 
 def layer_ops_supported(x: torch.Tensor) -> bool:
-    """Whether ``rms_norm`` / ``silu_mul`` take this activation: bf16 rows on the GPU."""
-    return x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1
+    """Whether ``rms_norm`` (x [N, D], D <= 8192) / ``silu_mul`` (x [N, 2F]) take this activation: bf16 rows on the
+    GPU, 16-byte aligned, the row length a multiple of 16 (of 8 for each half)."""
+    return (x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1 and x.stride(0) % 8 == 0
+            and x.size(1) % 16 == 0 and x.data_ptr() % 16 == 0)
+
+
+def rms_norm_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    return (layer_ops_supported(x) and x.size(1) <= 8192 and weight.dtype == x.dtype and weight.is_contiguous()
+            and weight.numel() == x.size(1) and weight.data_ptr() % 16 == 0)
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
@@ -481,9 +488,7 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     rounding after both products.  The norm of the reference's decoder layers (RMSNorm in
     src/omniasr_trt/modeling.py, run by SpecDecoder.step, spec.py:97-106)."""
     lib = _lib.load()
-    _need(layer_ops_supported(x) and x.stride(0) % 8 == 0, "rms_norm: bf16 x [N, D] with unit stride")
-    _need(weight.dtype == x.dtype and weight.is_contiguous() and weight.numel() == x.size(1),
-          "rms_norm: weight [D] in x's dtype")
+    _need(rms_norm_supported(x, weight), "rms_norm: bf16 x [N, D <= 8192] (16 | D, unit stride) and weight [D]")
     y = torch.empty(x.shape, device=x.device, dtype=x.dtype)
     status = lib.omni_rms_norm(x.data_ptr(), x.stride(0), weight.data_ptr(), y.data_ptr(), y.stride(0), x.size(0),
                                x.size(1), float(eps), _lib.BF16, _stream(x))
@@ -496,8 +501,7 @@ def silu_mul(gate_inner: torch.Tensor) -> torch.Tensor:
     rounded to bf16, then the product, as torch's two kernels round.  The FFN of the reference's decoder layers
     (spec.py:97-106 over the fused gate|inner projection of decode.py:34-54)."""
     lib = _lib.load()
-    _need(layer_ops_supported(gate_inner) and gate_inner.size(1) % 16 == 0 and gate_inner.stride(0) % 8 == 0,
-          "silu_mul: bf16 gate_inner [N, 2F] with F a multiple of 8")
+    _need(layer_ops_supported(gate_inner), "silu_mul: bf16 gate_inner [N, 2F] with F a multiple of 8")
     f = gate_inner.size(1) // 2
     out = torch.empty(gate_inner.size(0), f, device=gate_inner.device, dtype=gate_inner.dtype)
     status = lib.omni_silu_mul(gate_inner.data_ptr(), gate_inner.stride(0), out.data_ptr(), out.stride(0),
