@@ -224,8 +224,8 @@ def time_attention(pkg, torch, dec, t: int, reps: int, seed: int = 1003, separat
 
 def time_small_kernels(pkg, torch, dec, reps: int = 200) -> dict:
     """Config 2 RoPE + append (decode size and the 8 x 2048 prefill size), the causal prefill attention (8 x 2048),
-    the fused argmax + acceptance and the proposal, each timed with HIP events over ``reps`` launches
-    (latency-bound at decode sizes)."""
+    the fused argmax + acceptance, the proposal and the layers' norm and gate at the step's size, each timed with
+    HIP events over ``reps`` launches (latency-bound at decode sizes)."""
     kernels, spec = pkg.kernels, pkg.spec
     res = {}
     heads, dim = dec.heads, dec.head_dim
@@ -297,6 +297,21 @@ def time_small_kernels(pkg, torch, dec, reps: int = 200) -> dict:
             spec.AHEAD, spec.REACH, spec.SELF_WINDOW, spec.SELF_MIN)
     us = timed(lambda: kernels.spec_prepare(*args), reps)
     res["spec_prepare"] = {"us": round(us, 2)}
+    # The layers' element-wise ops at the step's size (one launch each; torch's ops beside them for reference).
+    layer = dec.m.llama_decoder.layers[0]
+    cfg = dec.m.dec_cfg
+    x = torch.randn(SLOTS * (DRAFT + 1), cfg.model_dim, device="cuda", generator=g).to(torch.bfloat16)
+    gi = torch.randn(SLOTS * (DRAFT + 1), 2 * cfg.ffn_dim, device="cuda", generator=g).to(torch.bfloat16)
+    norm = layer.self_attn_layer_norm
+    gate, inner = gi.chunk(2, -1)
+    for name, ours, theirs, nbytes in (
+            ("rms_norm_40x4096", lambda: kernels.rms_norm(x, norm.weight, norm.eps), lambda: norm(x),
+             x.numel() * 4 + norm.weight.numel() * 2),
+            ("silu_mul_40x11008", lambda: kernels.silu_mul(gi), lambda: inner * torch.nn.functional.silu(gate),
+             gi.numel() * 3)):
+        us, tus = timed(ours, reps), timed(theirs, reps)
+        res[name] = {"us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1),
+                     "torch_us": round(tus, 2)}
     return res
 
 
