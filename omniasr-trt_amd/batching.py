@@ -17,7 +17,7 @@ import torch
 from torch import Tensor, nn
 
 
-# ---------------------------------------------------------------------------------------------- weights
+# ---------------------------------------------------------------------------------------------- packed GEMM operands
 
 class LayerWeights(NamedTuple):
     """One decoder layer's GEMM operands ([out, in] each): q|k|v stacked, the attention output, gate|inner stacked,

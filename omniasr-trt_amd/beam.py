@@ -64,7 +64,8 @@ class BeamDecoder(GreedyDecoder):
         # Row state.  Scores in fp32 as the reference keeps them (fp64 for an fp64 model).
         self.score = torch.zeros(rows, dtype=torch.promote_types(torch.float32, self.dtype), device=dev)
         self.ended = torch.ones(rows, dtype=torch.bool, device=dev)
-        self.count = torch.zeros(rows, dtype=torch.long, device=dev)  # tokens other than PAD / EOS (length_norm)
+        # each row's real tokens so far: the length_norm divisor
+        self.count = torch.zeros(rows, dtype=torch.long, device=dev)
         # Group state: tokens chosen in the current context, the context's length, finished.
         self.k_step = torch.zeros(max_batch, dtype=torch.long, device=dev)
         self.ctx = torch.ones(max_batch, dtype=torch.long, device=dev)
@@ -80,7 +81,7 @@ class BeamDecoder(GreedyDecoder):
         self._normal_caps: tuple[int, int] | None = None
         self.stats["repetition_stops"] = 0
 
-    # ------------------------------------------------------------------ buffers
+    # ------------------------------------------------------------------ beam-side cache and search state
 
     def ensure_beam(self, ctx_len: int, gen_len: int) -> None:
         """Context caches for ``ctx_len`` positions per input, generated caches / pointers / histories for
@@ -115,7 +116,7 @@ class BeamDecoder(GreedyDecoder):
         self.ccap = self.gcap = 0
         self.reset_graphs()
 
-    # ------------------------------------------------------------------ one step
+    # ------------------------------------------------------------------ the search step
 
     def beam_state(self) -> list[Tensor]:
         """What a step changes besides the caches."""
@@ -167,7 +168,7 @@ class BeamDecoder(GreedyDecoder):
         self.stats["captures"] += self.graphs.captures - before
         return run
 
-    # ------------------------------------------------------------------ streams
+    # ------------------------------------------------------------------ scheduling beam groups over the inputs
 
     @torch.inference_mode()
     def decode_streams(self, n_streams: int, start, advance) -> None:

@@ -99,8 +99,9 @@ class GreedyDecoder:
         self.context_floor = CONTEXT_FLOOR
         self.use_graphs = graphs
         self.graphs = GraphCache(self.device, graphs)
-        self.debug_sync = os.environ.get("OMNIASR_TRT_DEBUG_SYNC") == "1"  # synchronise after each operation
-        self.phase = lambda name: nullcontext()  # the transcriber's timer when profiling
+        # OMNIASR_TRT_DEBUG_SYNC=1: wait for the device after every stage, so an error names the stage that raised it
+        self.debug_sync = os.environ.get("OMNIASR_TRT_DEBUG_SYNC") == "1"
+        self.phase = lambda name: nullcontext()  # context manager per named stage; a profiling caller replaces it
         self.stats = {"steps": 0, "rows_steps": 0, "tokens": 0, "prefill_tokens": 0, "captures": 0, "grows": 0}
         self.capacity = 0
         self.k = self.v = self.out = None
@@ -111,7 +112,7 @@ class GreedyDecoder:
         self.last = torch.zeros(rows, dtype=torch.long, device=dev)
         self.done = torch.ones(rows, dtype=torch.bool, device=dev)
 
-    # ------------------------------------------------------------------ persistent buffers
+    # ------------------------------------------------------------------ slot state kept across steps and graphs
 
     def ensure_capacity(self, length: int) -> None:
         """Make the KV cache and the token buffer hold ``length`` positions (rounded up to the key bucket, at most the
@@ -161,7 +162,7 @@ class GreedyDecoder:
     def _head(self, h: Tensor) -> Tensor:
         return self.m.final_proj(_norm(self.m.llama_decoder.layer_norm, h))
 
-    # ------------------------------------------------------------------ prefill
+    # ------------------------------------------------------------------ filling slots from their contexts
 
     def prefill(self, ctx: list[Tensor], slots: list[int] | None = None) -> Tensor:
         """Fill cache rows ``slots`` (default 0..B-1) with the contexts; returns each one's first token [B]."""
@@ -204,7 +205,7 @@ class GreedyDecoder:
         self.stats["prefill_tokens"] += int(lens.sum())
         return F.log_softmax(self._head(final), dim=-1)
 
-    # ------------------------------------------------------------------ one decode step
+    # ------------------------------------------------------------------ the step over every slot
 
     def layer_stack(self, h: Tensor, pos: Tensor, slots: Tensor | None, lengths: Tensor, tokens: int,
                     keys: int) -> Tensor:
@@ -247,7 +248,7 @@ class GreedyDecoder:
         self.stats["captures"] += self.graphs.captures - before
         return run
 
-    # ------------------------------------------------------------------ streams
+    # ------------------------------------------------------------------ scheduling inputs onto slots
 
     @torch.inference_mode()
     def generate(self, contexts: list[Tensor]) -> list[list[int]]:

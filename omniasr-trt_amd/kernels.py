@@ -396,7 +396,8 @@ def greedy_accept(logits: torch.Tensor, tokens: torch.Tensor, out: torch.Tensor,
                   start: torch.Tensor | None, use_draft: torch.Tensor | None, limit: int, eos: int,
                   nxt: torch.Tensor | None = None) -> torch.Tensor:
     """``F.log_softmax(logits, -1).argmax(-1)`` of the verify logits [B*T, V] followed by :func:`accept`
-    (src/omniasr_trt/spec.py:106-108): an argmax workgroup per row, then the acceptance.  Returns the argmaxes [B, T] (written into ``nxt`` when given).
+    (src/omniasr_trt/spec.py:106-108): an argmax workgroup per row, then the acceptance.  Returns the argmaxes
+    [B, T] (written into ``nxt`` when given).
     ``draft_next`` / ``start`` / ``use_draft`` None: the one-token step's update (src/omniasr_trt/decode.py:218-224)."""
     lib = _lib.load()
     b, width = tokens.shape

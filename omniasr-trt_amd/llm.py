@@ -18,7 +18,9 @@ from torch import Tensor
 from .modeling import HOP
 
 SEGMENT = 15 * 16000
-DRAFT_MARGIN = (25, 50)  # CTC frames before / after a segment's own in its draft (words across the boundary)
+# A segment's draft also takes this many CTC frames from before and after its own span, so that a word cut by the
+# segment boundary is still drafted whole.
+DRAFT_MARGIN = (25, 50)
 BOS, PAD, EOS = 0, 1, 2
 MAX_GEN = 8192
 CHECK_EVERY, CHECK_WINDOW, CHECK_RATIO = 250, 100, 4.0
@@ -65,7 +67,7 @@ class Row:
     segments: int
     lang: int = 0
     audio: list = field(default_factory=list)  # per segment: [F, D] decoder embeddings of its audio frames
-    tokens: list = field(default_factory=list)  # per segment: list[int]
+    tokens: list = field(default_factory=list)  # the decoded ids of each segment so far, one list per segment
     frames: np.ndarray | None = None  # draft source: CTC argmax of each 20 ms frame
 
     def draft(self, i: int) -> tuple[list[int], int] | None:

@@ -26,7 +26,8 @@ class DecoderConfig:
     num_heads: int = 8
     ffn_dim: int = 2816
     vocab_size: int = 10288
-    num_special: int = 3  # lid marker, last segment, regular segment (text embedding rows beyond the vocab)
+    # three marker ids after the vocabulary (language id, final segment, other segment): extra embedding rows
+    num_special: int = 3
     num_langs: int = 1694
     max_seq_len: int = 8192
     rope_theta: float = 10_000.0

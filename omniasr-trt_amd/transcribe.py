@@ -53,7 +53,7 @@ class Transcriber:
         self.device = model.final_proj.weight.device
         self._decoders: dict = {}
         self.last_decoder = None
-        self.profile = False  # synchronised wall time per phase in ``timings``
+        self.profile = False  # True: each phase synchronises the device and adds its seconds to ``timings``
         self.timings: dict[str, float] = {}
 
     @contextmanager
@@ -69,7 +69,7 @@ class Transcriber:
             torch.cuda.synchronize(self.device)
             self.timings[name] = self.timings.get(name, 0.0) + time.perf_counter() - t0
 
-    # ------------------------------------------------------------------ inputs
+    # ------------------------------------------------------------------ audio segments and prompts
 
     def rows(self, audio: list, langs=None, drafts=None) -> list[Row]:
         """One :class:`Row` per input: ``audio[j]`` the list of its segments' embeddings, ``langs[j]`` its language

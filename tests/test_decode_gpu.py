@@ -100,13 +100,13 @@ def test_same_tokens_as_greedy(cuda, draft_tokens):
     rng = np.random.default_rng(0)
     dec = SpecDecoder(m, draft_tokens=draft_tokens, max_batch=4, sync_every=3, reserve=8)
     say(f"spec k={draft_tokens}: perfect drafts")
-    assert run(dec, ctxs, [(r + [5, 6, 7], 0) for r in ref]) == ref  # perfect drafts running on past EOS
+    assert run(dec, ctxs, [(r + [5, 6, 7], 0) for r in ref]) == ref  # drafts that continue beyond the reference's EOS
     tokens_per_step = dec.stats["tokens"] / dec.stats["rows_steps"]
     say(f"spec k={draft_tokens}: noisy drafts ({tokens_per_step:.2f} tokens/row-step with perfect ones)")
     assert run(dec, ctxs, [(noisy(r, rng), 0) for r in ref]) == ref
     assert run(dec, ctxs, [(noisy(r[3:], rng), 2) for r in ref]) == ref  # starting mid-draft
     assert run(dec, ctxs, [None, ([], 0), *[(list(rng.integers(3, 12, 30)), 0) for _ in ctxs[2:]]]) == ref
-    if draft_tokens > 1:  # perfect drafts: several tokens per step
+    if draft_tokens > 1:  # exact drafts are accepted, so a row gains more than one token a step
         assert tokens_per_step > 1.5
 
 
