@@ -224,8 +224,8 @@ def time_attention(pkg, torch, dec, t: int, reps: int, seed: int = 1003, separat
 
 def time_small_kernels(pkg, torch, dec, reps: int = 200) -> dict:
     """Config 2 RoPE + append (decode size and the 8 x 2048 prefill size), the causal prefill attention (8 x 2048),
-    the fused argmax + acceptance, the proposal and the layers' norm and gate at the step's size, each timed with
-    HIP events over ``reps`` launches (latency-bound at decode sizes)."""
+    the fused argmax + acceptance, the proposal, the layers' norm and gate at the step's size and the beam step's
+    choice, each timed with HIP events over ``reps`` launches (latency-bound at decode sizes)."""
     kernels, spec = pkg.kernels, pkg.spec
     res = {}
     heads, dim = dec.heads, dec.head_dim
@@ -312,6 +312,26 @@ def time_small_kernels(pkg, torch, dec, reps: int = 200) -> dict:
         us, tus = timed(ours, reps), timed(theirs, reps)
         res[name] = {"us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1),
                      "torch_us": round(tus, 2)}
+    # The beam step's choice at config 5b's size (8 inputs x 5 beams): one launch against torch's log-softmax, the
+    # offers' element-wise ops and topk.
+    n, rows, vocab = BEAMS, SLOTS * BEAMS, cfg.vocab_size
+    lg = torch.randn(rows, vocab, device="cuda", generator=g).mul_(4).to(torch.bfloat16)
+    sc = -torch.rand(rows, device="cuda", generator=g) * 30
+    ct = torch.randint(1, 40, (rows,), device="cuda", generator=g)
+    en = torch.rand(rows, device="cuda", generator=g) < 0.2
+
+    def torch_select():
+        logp = torch.nn.functional.log_softmax(lg, dim=-1)
+        lead = ct.view(-1, n)[:, :1].expand(-1, n).reshape(-1, 1)
+        c = ct[:, None]
+        off = torch.where(lead > 0, (sc[:, None] * c + logp) / (c + 1), sc[:, None] + logp)
+        off = off.masked_fill(en[:, None], float("-inf"))
+        off[:, 2] = torch.where(en, sc, off[:, 2])
+        return off.view(SLOTS, n * vocab).topk(n, dim=-1, sorted=True)
+
+    us = timed(lambda: kernels.beam_select(lg, sc, ct, en, n, True, 2), reps)
+    res[f"beam_select_{SLOTS}x{n}x{vocab}"] = {"us": round(us, 2), "bytes": lg.numel() * 2,
+                                                "torch_us": round(timed(torch_select, reps), 2)}
     return res
 
 

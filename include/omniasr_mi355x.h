@@ -308,6 +308,26 @@ int omni_beam_take_over(int32_t groups, int32_t beams, int64_t vocab, const void
                         uint8_t *group_done, const int64_t *ctx, int64_t limit, int32_t eos, int32_t pad,
                         void *stream);
 
+/* Bytes of workspace omni_beam_select needs: groups x beams x beams pairs of 8 bytes. */
+size_t omni_beam_select_workspace(int32_t groups, int32_t beams);
+
+/*
+ * The beam step's choice (src/omniasr_trt/beam.py:165-175, after the LM head): for each of ``groups`` groups of
+ * ``beams`` rows of ``logits`` [groups * beams, vocab] (bf16, row stride ``logits_stride``), logp = log_softmax of
+ * each row (fp32 max and sum of exp, logsum = log(sum), logp = bf16((x - max) - logsum)); the offers
+ * score + logp, or with ``length_norm`` once the group's row 0 has count > 0, (score * count + logp) / (count + 1),
+ * each operation rounded to fp32 in that order; a row with ``ended`` set offers only EOS (``eos``), at its score;
+ * then best [groups, beams] fp32 and flat [groups, beams] int64 = offers.view(groups, beams * vocab).topk(beams),
+ * best first, equal values in the order of their flat index.  Replaces the reference's F.log_softmax, the offers'
+ * torch ops and torch.topk; the bookkeeping that follows is omni_beam_take_over.  score fp32 [rows], count int64
+ * [rows], ended uint8 [rows].  ``workspace``: omni_beam_select_workspace() bytes; ``tickets``: one int per group,
+ * zero, left zero.  beams 1..16; vocab a multiple of 8, at most 16384; dtype OMNI_BF16 (the logits).
+ */
+int omni_beam_select(const void *logits, int64_t logits_stride, int32_t groups, int32_t beams, int32_t vocab,
+                     const float *score, const int64_t *count, const uint8_t *ended, int32_t length_norm,
+                     int64_t eos, float *best, int64_t *flat, void *workspace, size_t workspace_bytes,
+                     int32_t *tickets, int32_t dtype, void *stream);
+
 /*
  * RMS norm of each row: y[r][i] = x[r][i] * rsqrt(sum_j x[r][j]^2 / dim + eps) * weight[i], fp32 arithmetic,
  * one rounding to bf16 after both products.  Replaces the torch kernel of the decoder layers' RMSNorm

@@ -52,6 +52,9 @@ _SIGNATURES = {
     "omni_greedy_accept": (c_int, [_P, c_int64, c_int32, c_int32, _P, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P,
                                    _P, c_int32, c_int32, c_int64, c_int64, _P]),
     "omni_beam_prepare": (c_int, [c_int32, c_int32, _P, _P, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P]),
+    "omni_beam_select_workspace": (c_size_t, [c_int32, c_int32]),
+    "omni_beam_select": (c_int, [_P, c_int64, c_int32, c_int32, c_int32, _P, _P, _P, c_int32, c_int64, _P, _P, _P,
+                                 c_size_t, _P, c_int32, _P]),
     "omni_rms_norm": (c_int, [_P, c_int64, _P, _P, c_int64, c_int32, c_int32, c_float, c_int32, _P]),
     "omni_silu_mul": (c_int, [_P, c_int64, _P, c_int64, c_int32, c_int32, c_int32, _P]),
     "omni_beam_take_over": (c_int, [c_int32, c_int32, c_int64, _P, _P, _P, c_int64, c_int64, _P, c_int64, c_int64,

@@ -137,7 +137,8 @@ class BeamDecoder(GreedyDecoder):
     def step_beam(self, s: int, ckeys: int) -> None:
         """One step of groups 0..s-1 (rows 0..s*N-1), in place; finished groups keep their state.  The bookkeeping
         before the layers and after the top-k runs in one launch each (``kernels.beam_prepare`` /
-        ``kernels.beam_take_over``).  (src/omniasr_trt/beam.py:127-187)"""
+        ``kernels.beam_take_over``), and for bf16 models the log-softmax, offers and top-k in one more
+        (``kernels.beam_select``).  (src/omniasr_trt/beam.py:127-187)"""
         n, r = self.beams, s * self.beams
         ptr = self.ptr[:r]
         kernels.beam_prepare(s, n, self.ctx, self.k_step, self.gdone, ptr, self.row_pos, self.gen_pos, self.ctx_len,
@@ -154,9 +155,14 @@ class BeamDecoder(GreedyDecoder):
                                               scale).reshape(r, -1)
 
             self._layer(i, h, attend)
-        logp = F.log_softmax(self._head(h), dim=-1)  # [R, V], model dtype
-        vocab = logp.size(-1)
-        best, flat = self._offers(logp, r).view(s, n * vocab).topk(n, dim=-1, sorted=True)  # [S, N], best first
+        logits = self._head(h)  # [R, V]
+        vocab = logits.size(-1)
+        if kernels.beam_select_supported(logits, self.score, n):  # bf16: log-softmax, offers and top-k in one launch
+            best, flat = kernels.beam_select(logits, self.score[:r], self.count[:r], self.ended[:r], n,
+                                             self.length_norm, EOS)
+        else:
+            logp = F.log_softmax(logits, dim=-1)  # model dtype
+            best, flat = self._offers(logp, r).view(s, n * vocab).topk(n, dim=-1, sorted=True)  # [S, N], best first
         kernels.beam_take_over(best, flat, vocab, ptr, self.hist[:r], self.ended, self.score, self.count, self.tok,
                                self.k_step, self.gdone, self.ctx, LIMIT, EOS, PAD)
 

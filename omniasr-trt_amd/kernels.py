@@ -40,6 +40,7 @@ DRAFT_ATTN = {"chunk": 0, "separate": True, "split_k": False}
 ATTN = {"chunk": 0, "separate": True, "split_k": False}
 
 _counters: dict[int, torch.Tensor] = {}
+_select_tickets: dict[int, torch.Tensor] = {}
 # Ticket buffers replaced by larger ones: captured graphs may still hold their addresses, so they
 # live as long as the process.
 _retired: list[torch.Tensor] = []
@@ -110,19 +111,24 @@ def rope_kv(qkv: torch.Tensor, cs: torch.Tensor, pos: torch.Tensor, k_cache: tor
     return q
 
 
-def _attn_counters(device: torch.device, n: int) -> torch.Tensor:
-    """Per-(row, head) tickets of the split merge: zero, and left zero by every call."""
+def _tickets(store: dict, device: torch.device, n: int, what: str, least: int) -> torch.Tensor:
+    """At least ``n`` int32 tickets on ``device`` from ``store``: zero, and left zero by every call."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    have = _counters.get(idx)
+    have = store.get(idx)
     if have is None or have.numel() < n:
         if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("verify attention: its tickets must be allocated before graph capture "
+            raise RuntimeError(f"{what}: its tickets must be allocated before graph capture "
                                "(run the step once outside the capture)")
-        size = max(n, 1 << 16, 0 if have is None else 2 * have.numel())
+        size = max(n, least, 0 if have is None else 2 * have.numel())
         if have is not None:
             _retired.append(have)
-        _counters[idx] = have = torch.zeros(size, device=device, dtype=torch.int32)
+        store[idx] = have = torch.zeros(size, device=device, dtype=torch.int32)
     return have
+
+
+def _attn_counters(device: torch.device, n: int) -> torch.Tensor:
+    """Per-(row, head) tickets of the split merge."""
+    return _tickets(_counters, device, n, "verify attention", 1 << 16)
 
 
 def _verify(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor, tokens: int,
@@ -470,6 +476,44 @@ def beam_take_over(best: torch.Tensor, flat: torch.Tensor, vocab: int, ptr: torc
                                      tok.data_ptr(), k_step.data_ptr(), group_done.data_ptr(), ctx.data_ptr(),
                                      int(limit), int(eos), int(pad), _stream(best))
     _lib.check(status, "beam_take_over")
+
+
+def beam_select_supported(logits: torch.Tensor, score: torch.Tensor, beams: int) -> bool:
+    """Whether ``beam_select`` takes these logits: bf16 [rows, V] on the GPU (unit stride, 16-byte aligned rows, V a
+    multiple of 8, at most 16384), fp32 scores, 1..16 beams."""
+    return (logits.is_cuda and logits.dtype == torch.bfloat16 and logits.dim() == 2 and logits.stride(1) == 1
+            and logits.stride(0) % 8 == 0 and logits.data_ptr() % 16 == 0 and logits.size(1) % 8 == 0
+            and beams <= logits.size(1) <= 16384 and 1 <= beams <= 16 and score.dtype == torch.float32)
+
+
+def beam_select(logits: torch.Tensor, score: torch.Tensor, count: torch.Tensor, ended: torch.Tensor, beams: int,
+                length_norm: bool, eos: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """The beam step's choice in one launch (src/omniasr_trt/beam.py:165-175): ``F.log_softmax(logits)`` in bf16,
+    the offers (score + logp; with ``length_norm``, once the group's row 0 has tokens, (score * count + logp) /
+    (count + 1); a finished row offers only ``eos``, at its score) and ``offers.view(S, N * V).topk(N)`` -- returns
+    (best [S, N] fp32, flat [S, N] int64), best first, equal values in the order of their flat index.  ``score`` /
+    ``count`` / ``ended``: the rows' state (fp32 / int64 / bool, at least S * N rows)."""
+    lib = _lib.load()
+    _need(beam_select_supported(logits, score, beams), "beam_select: bf16 logits [S*N, V] (8 | V <= 16384, unit "
+          "stride), fp32 score, 1..16 beams")
+    rows, vocab = logits.shape
+    _need(rows % beams == 0, "beam_select: rows a multiple of beams")
+    _need(score.is_contiguous() and score.numel() >= rows, "score: fp32 [>= rows]")
+    _index(count, "count")
+    _flags(ended, "ended")
+    _need(count.numel() >= rows and ended.numel() >= rows, "count / ended: [>= rows]")
+    groups = rows // beams
+    best = torch.empty(groups, beams, device=logits.device, dtype=torch.float32)
+    flat = torch.empty(groups, beams, device=logits.device, dtype=torch.long)
+    ws = lib.omni_beam_select_workspace(groups, beams)
+    workspace = torch.empty(max(ws, 256), device=logits.device, dtype=torch.uint8)
+    tickets = _tickets(_select_tickets, logits.device, groups, "beam_select", 256)
+    status = lib.omni_beam_select(logits.data_ptr(), logits.stride(0), groups, beams, vocab, score.data_ptr(),
+                                  count.data_ptr(), ended.data_ptr(), int(bool(length_norm)), int(eos),
+                                  best.data_ptr(), flat.data_ptr(), workspace.data_ptr(), workspace.numel(),
+                                  tickets.data_ptr(), _lib.BF16, _stream(logits))
+    _lib.check(status, "beam_select")
+    return best, flat
 
 
 def layer_ops_supported(x: torch.Tensor) -> bool:
