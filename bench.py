@@ -410,8 +410,9 @@ def beam_leg(pkg, torch, w: Workload, steps: int, warmup: int, reps: int) -> dic
 
 
 def time_prefill_real(pkg, torch, caches, width: int = 2048, reps: int = 10) -> dict:
-    """The causal prefill at the real checkpoint's shape (8 contexts x ``width`` positions x 8 heads x 512, bf16):
-    one launch of the wide-head causal kernel per call, three untimed calls first (eager, HIP events)."""
+    """The causal prefill of 8 contexts x ``width`` positions at the caches' heads x head dim (the real checkpoint:
+    8 x 512), bf16: one launch of the causal kernel per call, three untimed calls first (eager, HIP events); torch's
+    fused scaled_dot_product_attention (flash / memory-efficient backends) timed the same way beside it."""
     kernels = pkg.kernels
     heads, dim = caches.heads, caches.head_dim
     g = torch.Generator(device="cuda").manual_seed(1007)
@@ -429,8 +430,30 @@ def time_prefill_real(pkg, torch, caches, width: int = 2048, reps: int = 10) -> 
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1000.0 / reps
     flops = 4 * dim * heads * SLOTS * width * (width + 1) // 2
-    return {"us": round(us, 1), "flops": flops, "TFLOPs": round(flops / us / 1e6, 1),
-            "frac_bf16_peak": round(flops / us / 1e6 / 2500.0, 4)}
+    res = {"us": round(us, 1), "flops": flops, "TFLOPs": round(flops / us / 1e6, 1),
+           "frac_bf16_peak": round(flops / us / 1e6 / 2500.0, 4)}
+    # torch's own fused attention on the same q / K / V for comparison: the flash or memory-efficient backend only
+    # (the math path is never run: it would materialise the score matrix in bf16 batched products).
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    qt = q.view(SLOTS, width, heads, dim).transpose(1, 2)
+    kt, vt = caches.k[0][:SLOTS, :, :width], caches.v[0][:SLOTS, :, :width]
+    for name, backend in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel([backend]):
+                sdpa = lambda: torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, is_causal=True)
+                for _ in range(3):
+                    sdpa()
+                torch.cuda.synchronize()
+                e0.record()
+                for _ in range(reps):
+                    sdpa()
+                e1.record()
+                torch.cuda.synchronize()
+            res[f"torch_sdpa_{name}_us"] = round(e0.elapsed_time(e1) * 1000.0 / reps, 1)
+        except RuntimeError as e:  # backend not built for this shape / dtype
+            res[f"torch_sdpa_{name}_us"] = None
+            res[f"torch_sdpa_{name}_error"] = str(e).splitlines()[0][:120]
+    return res
 
 
 def time_beam_attention(pkg, torch, reps: int, layers: int = 12, seed: int = 1006, heads: int = 32,
