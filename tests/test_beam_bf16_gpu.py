@@ -9,6 +9,9 @@ between the best offers of different hypotheses fall far below the bf16 error.  
   beam gives exactly the fp64 reference-order loop's tokens;
 * inside a 5-beam search (length normalisation on), the beam attention of the first and the last layer is recorded
   at every step and checked against ``oracle.verify.beam_attention`` on the same inputs (2e-2 abs / 1e-2 rel);
+* every step's choice (the log-softmax, offers and top-k in one launch) equals the choice made on torch's own ops
+  over the same logits and state, in nearly every group (printed and bounded), and its values are within one bf16
+  step of logp of that choice's everywhere, with and without length normalisation;
 * graph replays of the beam step equal eager steps (same tokens, same steps).
 """
 
@@ -67,6 +70,42 @@ def test_beam_attention_inside_the_search(shape, monkeypatch):  # noqa: F811
     texts = dec.generate(ctxs)
     say(f"{name}: 5 beams, {len(checked)} beam-attention calls checked (context, generated keys): {checked[:6]} ...")
     assert len(checked) >= 12 and max(g for _, g in checked) >= 3
+    assert len(texts) == len(ctxs)
+
+
+@pytest.mark.parametrize("length_norm", [True, False])
+def test_beam_choice_inside_the_search(shape, monkeypatch, length_norm):  # noqa: F811
+    """Every step's choice (``kernels.beam_select``: log-softmax, offers, top-k in one launch) against the choice
+    made on torch's own ops over the same logits and the search's state at that step."""
+    from test_beam_select_gpu import EOS, choose, torch_offers
+
+    name, m, ctxs, refs = shape
+    real = kernels.beam_select
+    seen = {"groups": 0, "same": 0, "calls": 0}
+
+    def recorded(logits, score, count, ended, beams, norm, eos):
+        best, flat = real(logits, score, count, ended, beams, norm, eos)
+        assert eos == EOS and norm == length_norm
+        rows = logits.size(0)
+        offers, _ = torch_offers(logits, score[:rows], count[:rows], ended[:rows], beams, norm)
+        want_best, want_flat = choose(offers.view(rows // beams, -1).cpu().numpy(), beams)
+        got_best, got_flat = best.cpu().numpy(), flat.cpu().numpy()
+        fin = np.isfinite(want_best)
+        assert (np.isfinite(got_best) == fin).all()
+        # a different choice only between offers within a bf16 step of logp of each other
+        assert (np.abs(got_best - want_best)[fin] <= np.abs(want_best[fin]) * 2.0 ** -7 + 1e-6).all()
+        seen["calls"] += 1
+        seen["groups"] += len(want_flat)
+        seen["same"] += int(sum((got_flat[i] == want_flat[i]).all() and (got_best[i] == want_best[i]).all()
+                                for i in range(len(want_flat))))
+        return best, flat
+
+    monkeypatch.setattr(kernels, "beam_select", recorded)
+    dec = BeamDecoder(m, beams=5, length_norm=length_norm, max_batch=8, sync_every=4, reserve=16, graphs=False)
+    texts = dec.generate(ctxs)
+    say(f"{name}: length_norm={length_norm}: {seen['calls']} beam steps, {seen['same']} of {seen['groups']} group "
+        f"choices identical to the choice on torch's offers")
+    assert seen["calls"] >= 8 and seen["same"] >= 0.95 * seen["groups"]
     assert len(texts) == len(ctxs)
 
 
