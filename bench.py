@@ -224,7 +224,7 @@ def time_attention(pkg, torch, dec, t: int, reps: int, seed: int = 1003, separat
 
 def time_small_kernels(pkg, torch, dec, reps: int = 200) -> dict:
     """Config 2 RoPE + append (decode size and the 8 x 2048 prefill size), the causal prefill attention (8 x 2048),
-    the fused argmax + acceptance, the proposal, the layers' norm and gate at the step's size and the beam step's
+    the fused argmax + acceptance, config 1's verify step (one slot), the proposal, the layers' norm and gate at the step's size and the beam step's
     choice, each timed with HIP events over ``reps`` launches (latency-bound at decode sizes)."""
     kernels, spec = pkg.kernels, pkg.spec
     res = {}
@@ -291,6 +291,28 @@ def time_small_kernels(pkg, torch, dec, reps: int = 200) -> dict:
     us = timed(lambda: kernels.greedy_accept(logits, tokens, *st, None, None, None, 8188, 2), reps)
     nbytes = logits.numel() * 2
     res["greedy_accept"] = {"us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1)}
+    # Config 1: one slot's verify step, 1 + 4 queries over 1024 prior keys (32 x 128, bf16), then its acceptance
+    # over [5, V] logits.
+    # 16 disjoint caches (17 MB each) cycled per call, so the 256 MB Infinity Cache cannot serve them.
+    t1, n1, sets = DRAFT + 1, 1024, 16
+    kv1 = [(torch.randn(1, heads, n1 + 64, dim, device="cuda", generator=g).to(torch.bfloat16),
+            torch.randn(1, heads, n1 + 64, dim, device="cuda", generator=g).to(torch.bfloat16)) for _ in range(sets)]
+    q1 = torch.randn(t1, heads, dim, device="cuda", generator=g).to(torch.bfloat16)
+    len1 = torch.tensor([n1], device="cuda")
+    turn = [0]
+
+    def config1_attention():
+        kc1, vc1 = kv1[turn[0] % sets]
+        turn[0] += 1
+        return kernels.draft_attention(q1, kc1, vc1, len1, t1, n1 + t1, dim ** -0.5)
+
+    us_a = timed(config1_attention, reps)
+    st1 = [x[:1] for x in st]
+    us_g = timed(lambda: kernels.greedy_accept(logits[:t1], tokens[:1], *st1, None, None, None, 8188, 2), reps)
+    nbytes = heads * dim * 2 * 2 * (n1 + t1 - 1) + 2 * t1 * heads * dim * 2
+    res["config1_verify_step"] = {"attention_us": round(us_a, 2), "attention_bytes": nbytes,
+                                  "attention_GBps": round(nbytes / us_a / 1e3, 1),
+                                  "greedy_accept_us": round(us_g, 2), "us": round(us_a + us_g, 2)}
     b = SLOTS
     args = (dec.out[:b], dec.draft[:b], dec.draft_len[:b], dec.last[:b], dec.first[:b], dec.next[:b],
             dec.start[:b].clone(), dec.tok[:b], dec.done[:b], dec.capacity, DRAFT, spec.NGRAM, spec.BEHIND,
