@@ -136,12 +136,23 @@ int omni_verify_attention(const void *q, const void *k_cache, const void *v_cach
  * launches what omni_verify_attention launches.  Every call on a GPU shares that GPU's array: calls that
  * overlap in time on one GPU (other streams, other threads) race and must not be made.  The array used is the
  * current device's (hipGetDevice), so ``stream`` must belong to the current device, as the caller's buffers do.
+ * The array's device address is looked up once per device, by omni_verify_attention_static_init or else by the
+ * first call on the device; a first call whose stream is being captured returns OMNI_ERR_INVALID without
+ * launching anything (the lookup may load the code object, which a capture must not record).
  */
 int omni_verify_attention_static(const void *q, const void *k_cache, const void *v_cache,
                                  int64_t stride_row, int64_t stride_head, int64_t stride_pos,
                                  int64_t cache_len, const int64_t *lengths, int32_t rows, int32_t tokens,
                                  int32_t heads, int32_t head_dim, int32_t keys, int32_t chunk, float scale,
                                  void *out, int32_t flags, int32_t dtype, void *stream);
+
+/*
+ * Set-up of omni_verify_attention_static on the current device: looks up the device address of its static array
+ * (hipGetSymbolAddress) and keeps it.  Call it once per device, with that device current, before any graph
+ * capture that records omni_verify_attention_static.  No counterpart in the reference; for the same callers
+ * (those that cannot allocate).  Allocates nothing.
+ */
+int omni_verify_attention_static_init(void);
 
 /* Bytes of workspace omni_beam_attention needs for this shape and split size (0: default). */
 size_t omni_beam_attention_workspace(int32_t groups, int32_t beams, int32_t heads, int32_t head_dim,
@@ -311,22 +322,29 @@ int omni_beam_take_over(int32_t groups, int32_t beams, int64_t vocab, const void
 /* Bytes of workspace omni_beam_select needs: groups x beams x beams pairs of 8 bytes. */
 size_t omni_beam_select_workspace(int32_t groups, int32_t beams);
 
+/* What omni_beam_select's input rows hold. */
+#define OMNI_SELECT_LOGP 0   /* log-probabilities (the caller's F.log_softmax): the choice is the reference's exactly */
+#define OMNI_SELECT_LOGITS 1 /* logits: the log-softmax runs in the kernel, in its own summation order */
+
 /*
  * The beam step's choice (src/omniasr_trt/beam.py:165-175, after the LM head): for each of ``groups`` groups of
- * ``beams`` rows of ``logits`` [groups * beams, vocab] (bf16, row stride ``logits_stride``), logp = log_softmax of
- * each row (fp32 max and sum of exp, logsum = log(sum), logp = bf16((x - max) - logsum)); the offers
- * score + logp, or with ``length_norm`` once the group's row 0 has count > 0, (score * count + logp) / (count + 1),
- * each operation rounded to fp32 in that order; a row with ``ended`` set offers only EOS (``eos``), at its score;
- * then best [groups, beams] fp32 and flat [groups, beams] int64 = offers.view(groups, beams * vocab).topk(beams),
- * best first, equal values in the order of their flat index.  Replaces the reference's F.log_softmax, the offers'
- * torch ops and torch.topk; the bookkeeping that follows is omni_beam_take_over.  score fp32 [rows], count int64
- * [rows], ended uint8 [rows].  ``workspace``: omni_beam_select_workspace() bytes; ``tickets``: one int per group,
- * zero, left zero.  beams 1..16; vocab a multiple of 8, at most 16384; dtype OMNI_BF16 (the logits).
+ * ``beams`` rows of ``logits`` [groups * beams, vocab] (bf16, row stride ``logits_stride``), logp = the rows
+ * themselves (``input_kind`` OMNI_SELECT_LOGP: the output of the reference's own F.log_softmax, beam.py:162) or the
+ * log_softmax of each row computed here (OMNI_SELECT_LOGITS: fp32 max and sum of exp in this kernel's order,
+ * logsum = log(sum), logp = bf16((x - max) - logsum); a logp on a bf16 rounding boundary can round differently from
+ * torch's); the offers score + logp, or with ``length_norm`` once the group's row 0 has count > 0,
+ * (score * count + logp) / (count + 1), each operation rounded to fp32 in that order; a row with ``ended`` set
+ * offers only EOS (``eos``), at its score; then best [groups, beams] fp32 and flat [groups, beams] int64 =
+ * offers.view(groups, beams * vocab).topk(beams), best first, equal values in the order of their flat index.
+ * Replaces the offers' torch ops and torch.topk (and, with OMNI_SELECT_LOGITS, F.log_softmax); the bookkeeping that
+ * follows is omni_beam_take_over.  score fp32 [rows], count int64 [rows], ended uint8 [rows].  ``workspace``:
+ * omni_beam_select_workspace() bytes; ``tickets``: one int per group, zero, left zero (calls that overlap on one
+ * GPU need tickets of their own).  beams 1..16; vocab a multiple of 8, at most 16384; dtype OMNI_BF16.
  */
 int omni_beam_select(const void *logits, int64_t logits_stride, int32_t groups, int32_t beams, int32_t vocab,
                      const float *score, const int64_t *count, const uint8_t *ended, int32_t length_norm,
                      int64_t eos, float *best, int64_t *flat, void *workspace, size_t workspace_bytes,
-                     int32_t *tickets, int32_t dtype, void *stream);
+                     int32_t *tickets, int32_t input_kind, int32_t dtype, void *stream);
 
 /*
  * RMS norm of each row: y[r][i] = x[r][i] * rsqrt(sum_j x[r][j]^2 / dim + eps) * weight[i], fp32 arithmetic,

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: its HIP runtime is the one the library uses)
 
 PATH = Path(__file__).resolve().with_name("libomniasr_mi355x.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK = 0
 F32, BF16 = 0, 1
@@ -22,6 +22,7 @@ ATTN_SEPARATE_COMBINE = 1
 ATTN_SPLIT_K = 2
 STATIC_WORKSPACE_BYTES = 32 << 20  # OMNI_STATIC_WORKSPACE_BYTES
 STATIC_MAX_UNITS = 16384  # OMNI_STATIC_MAX_UNITS
+SELECT_LOGP, SELECT_LOGITS = 0, 1  # OMNI_SELECT_*: what omni_beam_select's input rows hold
 
 _P = c_void_p
 _SIGNATURES = {
@@ -36,6 +37,7 @@ _SIGNATURES = {
                                       _P]),
     "omni_verify_attention_static": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, c_int32, c_int32,
                                              c_int32, c_int32, c_int32, c_int32, c_float, _P, c_int32, c_int32, _P]),
+    "omni_verify_attention_static_init": (c_int, []),
     "omni_beam_attention_workspace": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
     "omni_beam_attention": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, c_int64, c_int64,
                                     c_int64, c_int64, c_int64, _P, c_int64, _P, c_int32, c_int32, c_int32, c_int32,
@@ -54,7 +56,7 @@ _SIGNATURES = {
     "omni_beam_prepare": (c_int, [c_int32, c_int32, _P, _P, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P]),
     "omni_beam_select_workspace": (c_size_t, [c_int32, c_int32]),
     "omni_beam_select": (c_int, [_P, c_int64, c_int32, c_int32, c_int32, _P, _P, _P, c_int32, c_int64, _P, _P, _P,
-                                 c_size_t, _P, c_int32, _P]),
+                                 c_size_t, _P, c_int32, c_int32, _P]),
     "omni_rms_norm": (c_int, [_P, c_int64, _P, _P, c_int64, c_int32, c_int32, c_float, c_int32, _P]),
     "omni_silu_mul": (c_int, [_P, c_int64, _P, c_int64, c_int32, c_int32, c_int32, _P]),
     "omni_beam_take_over": (c_int, [c_int32, c_int32, c_int64, _P, _P, _P, c_int64, c_int64, _P, c_int64, c_int64,

@@ -80,6 +80,9 @@ class BeamDecoder(GreedyDecoder):
         self.ccap = self.gcap = 0
         self._normal_caps: tuple[int, int] | None = None
         self.stats["repetition_stops"] = 0
+        # This search's own merge tickets of the choice (one per group, zero between launches), so that two searches
+        # on different streams of one GPU never share them.
+        self.select_tickets = torch.zeros(max_batch, dtype=torch.int32, device=dev)
 
     # ------------------------------------------------------------------ beam-side cache and search state
 
@@ -157,9 +160,9 @@ class BeamDecoder(GreedyDecoder):
             self._layer(i, h, attend)
         logits = self._head(h)  # [R, V]
         vocab = logits.size(-1)
-        if kernels.beam_select_supported(logits, self.score, n):  # bf16: log-softmax, offers and top-k in one launch
+        if kernels.beam_select_supported(logits, self.score, n):  # bf16: torch's log-softmax, then offers + top-k
             best, flat = kernels.beam_select(logits, self.score[:r], self.count[:r], self.ended[:r], n,
-                                             self.length_norm, EOS)
+                                             self.length_norm, EOS, tickets=self.select_tickets)
         else:
             logp = F.log_softmax(logits, dim=-1)  # model dtype
             best, flat = self._offers(logp, r).view(s, n * vocab).topk(n, dim=-1, sorted=True)  # [S, N], best first

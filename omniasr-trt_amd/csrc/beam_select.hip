@@ -1,7 +1,10 @@
 // The beam search step's choice, for gfx950: each group's N best offers over its N rows x V tokens, from the LM
-// head's logits (src/omniasr_trt/beam.py:165-175):
-//   logp  = log_softmax(logits) per row, in the model's dtype (bf16): fp32 max, fp32 sum of exp(x - max),
-//           logsum = log(sum), logp = bf16((x - max) - logsum) -- the arithmetic of torch's log-softmax kernel;
+// head's log-probabilities or logits (src/omniasr_trt/beam.py:165-175):
+//   logp  = the input itself (OMNI_SELECT_LOGP: torch's own F.log_softmax output, so the choice is the reference's
+//           bit for bit), or (OMNI_SELECT_LOGITS) log_softmax(logits) per row computed here in the model's dtype
+//           (bf16): fp32 max, fp32 sum of exp(x - max) in this kernel's own order, logsum = log(sum),
+//           logp = bf16((x - max) - logsum) -- the arithmetic of torch's kernel but not its summation order, so a
+//           logp on a bf16 rounding boundary can round the other way;
 //   offer = score + logp, or with length_norm, once the group's row 0 has tokens, (score * count + logp) / (count + 1),
 //           each operation rounded to fp32 in that order (torch's element-wise kernels, no fused multiply-add);
 //           a finished row offers -inf everywhere except EOS, at its frozen score;
@@ -95,6 +98,7 @@ struct SelectArgs {
   int64_t* flat;
   uint64_t* cand;  // [rows][beams] keys of each row's best, written through
   int* tickets;    // [groups], zero before and after
+  int logp_in;     // 1: the input rows are log-probabilities already (no log-softmax here)
 };
 
 // CPT: 8-logit chunks per thread (V <= 8 x 256 x CPT).
@@ -118,23 +122,26 @@ __global__ __launch_bounds__(kSelThreads) void beam_select_kernel(SelectArgs a) 
   const bool ended = a.ended[row] != 0;
   const bool norm = a.length_norm && a.count[(int64_t)g * n] > 0;
 
-  float m = -INFINITY;
+  float m = 0.f, logsum = 0.f;
+  if (!a.logp_in) {  // block-uniform
+    m = -INFINITY;
 #pragma unroll
-  for (int c = 0; c < CPT; ++c)
-    if ((tid + c * kSelThreads) * 8 < V) {
+    for (int c = 0; c < CPT; ++c)
+      if ((tid + c * kSelThreads) * 8 < V) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) m = fmaxf(m, bf16x8_elem(x[c], e));
-    }
-  m = sel_block_reduce(m, red, true);
-  float sum = 0.f;
+        for (int e = 0; e < 8; ++e) m = fmaxf(m, bf16x8_elem(x[c], e));
+      }
+    m = sel_block_reduce(m, red, true);
+    float sum = 0.f;
 #pragma unroll
-  for (int c = 0; c < CPT; ++c)
-    if ((tid + c * kSelThreads) * 8 < V) {
+    for (int c = 0; c < CPT; ++c)
+      if ((tid + c * kSelThreads) * 8 < V) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sum += expf(bf16x8_elem(x[c], e) - m);
-    }
-  sum = sel_block_reduce(sum, red, false);
-  const float logsum = logf(sum);
+        for (int e = 0; e < 8; ++e) sum += expf(bf16x8_elem(x[c], e) - m);
+      }
+    sum = sel_block_reduce(sum, red, false);
+    logsum = logf(sum);
+  }
 
   // The row's offers as keys with their flat indices in the group's N x V (past V: key 0, never chosen).
   uint64_t keys[CPT * 8];
@@ -144,7 +151,7 @@ __global__ __launch_bounds__(kSelThreads) void beam_select_kernel(SelectArgs a) 
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int v = (tid + c * kSelThreads) * 8 + e;
-      const float lp = round_through_bf16((bf16x8_elem(x[c], e) - m) - logsum);
+      const float lp = a.logp_in ? bf16x8_elem(x[c], e) : round_through_bf16((bf16x8_elem(x[c], e) - m) - logsum);
       float o;
       if (norm) {
         const float t = score * cf;
@@ -207,8 +214,10 @@ extern "C" size_t omni_beam_select_workspace(int32_t groups, int32_t beams) {
 extern "C" int omni_beam_select(const void* logits, int64_t logits_stride, int32_t groups, int32_t beams,
                                 int32_t vocab, const float* score, const int64_t* count, const uint8_t* ended,
                                 int32_t length_norm, int64_t eos, float* best, int64_t* flat, void* workspace,
-                                size_t workspace_bytes, int32_t* tickets, int32_t dtype, void* stream) {
+                                size_t workspace_bytes, int32_t* tickets, int32_t input_kind, int32_t dtype,
+                                void* stream) {
   if (dtype != OMNI_BF16) return OMNI_ERR_DTYPE;
+  if (input_kind != OMNI_SELECT_LOGP && input_kind != OMNI_SELECT_LOGITS) return OMNI_ERR_INVALID;
   if (groups < 0 || beams < 1 || beams > omni::kSelMaxBeams || vocab < beams) return OMNI_ERR_INVALID;
   if (vocab % 8 != 0 || vocab > 8 * omni::kSelThreads * 8) return OMNI_ERR_SHAPE;
   if (groups == 0) return OMNI_OK;
@@ -218,7 +227,8 @@ extern "C" int omni_beam_select(const void* logits, int64_t logits_stride, int32
     return OMNI_ERR_INVALID;
   if (!workspace || workspace_bytes < omni_beam_select_workspace(groups, beams)) return OMNI_ERR_WORKSPACE;
   omni::SelectArgs a{static_cast<const uint16_t*>(logits), logits_stride, beams, vocab, score, count, ended,
-                     length_norm, eos, best, flat, static_cast<uint64_t*>(workspace), tickets};
+                     length_norm, eos, best, flat, static_cast<uint64_t*>(workspace), tickets,
+                     input_kind == OMNI_SELECT_LOGP ? 1 : 0};
   const int rows = groups * beams, cpt = (vocab / 8 + omni::kSelThreads - 1) / omni::kSelThreads;
   hipStream_t s = (hipStream_t)stream;
   if (cpt <= 2)

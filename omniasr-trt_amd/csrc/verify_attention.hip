@@ -1520,14 +1520,22 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch[kMaxDevices];
 
-// This device's copy of ``scratch`` (looked up on the first call made with the device current).
-int scratch_address(void** ptr) {
+// This device's copy of ``scratch``: looked up by omni_verify_attention_static_init, or by the entry point's first
+// call with the device current when that call's stream is not being captured (the lookup may load the code object,
+// which a capture must not record).  ``stream`` null: the caller is the init call, nothing is being captured.
+int scratch_address(void** ptr, hipStream_t stream, bool check_capture) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return (int)e;
   if (dev < 0 || dev >= kMaxDevices) return OMNI_ERR_INVALID;
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (g_scratch[dev] == nullptr) {
+    if (check_capture) {
+      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+      e = hipStreamIsCapturing(stream, &cap);
+      if (e != hipSuccess) return (int)e;
+      if (cap != hipStreamCaptureStatusNone) return OMNI_ERR_INVALID;  // omni_verify_attention_static_init first
+    }
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return (int)e;
@@ -1543,6 +1551,11 @@ __global__ __launch_bounds__(256) void zero_tickets_kernel(int32_t* p, int n) {
 }
 
 }  // namespace
+
+extern "C" int omni_verify_attention_static_init(void) {
+  void* base = nullptr;
+  return scratch_address(&base, nullptr, false);
+}
 
 extern "C" int omni_verify_attention_static(const void* q, const void* k_cache, const void* v_cache,
                                             int64_t stride_row, int64_t stride_head, int64_t stride_pos,
@@ -1562,7 +1575,7 @@ extern "C" int omni_verify_attention_static(const void* q, const void* k_cache, 
   const int64_t units = (int64_t)rows * heads;
   if (need > OMNI_STATIC_WORKSPACE_BYTES || units > OMNI_STATIC_MAX_UNITS) return OMNI_ERR_WORKSPACE;
   void* base = nullptr;
-  st = scratch_address(&base);
+  st = scratch_address(&base, (hipStream_t)stream, true);
   if (st != OMNI_OK) return st;
   int32_t* tickets = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(base) + OMNI_STATIC_WORKSPACE_BYTES);
   // The tickets must be zero when the attention starts.  Every call leaves them zero, but the array keeps whatever

@@ -28,6 +28,7 @@ from __future__ import annotations
 import ctypes
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib
 
@@ -159,14 +160,33 @@ def _verify(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengt
     return out
 
 
+_static_ready: set[int] = set()
+
+
+def static_init(device: torch.device) -> None:
+    """Set-up of :func:`verify_attention_static` on ``device`` (``omni_verify_attention_static_init``, once per
+    device, outside graph capture): the library's static scratch gets its device address."""
+    device = torch.device(device)
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx in _static_ready:
+        return
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("verify_attention_static: call kernels.static_init(device) before graph capture")
+    with torch.cuda.device(idx):
+        _lib.check(_lib.load().omni_verify_attention_static_init(), "verify attention static scratch set-up")
+    _static_ready.add(idx)
+
+
 def verify_attention_static(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor,
                             tokens: int, keys: int, scale: float, out: torch.Tensor, chunk: int = 0,
                             separate: bool = True, split_k: bool = False) -> torch.Tensor:
     """:func:`draft_attention` into the caller's ``out`` (same shape and dtype as ``q``) with nothing allocated: the
     library's per-GPU static scratch holds the split partials and tickets (``omni_verify_attention_static``).  Shapes
     whose workspace exceeds ``_lib.STATIC_WORKSPACE_BYTES`` (or with rows x heads > ``_lib.STATIC_MAX_UNITS``) raise.
-    Calls that overlap in time on one GPU race: they share its scratch."""
+    Calls that overlap in time on one GPU race: they share its scratch.  The scratch's address is looked up by the
+    first call on each device (``omni_verify_attention_static_init``), which must not be under graph capture."""
     lib = _lib.load()
+    static_init(q.device)
     rows_total, heads, dim = q.shape
     _need(rows_total % tokens == 0, "q: [B*T, H, D]")
     groups = rows_total // tokens
@@ -487,12 +507,20 @@ def beam_select_supported(logits: torch.Tensor, score: torch.Tensor, beams: int)
 
 
 def beam_select(logits: torch.Tensor, score: torch.Tensor, count: torch.Tensor, ended: torch.Tensor, beams: int,
-                length_norm: bool, eos: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """The beam step's choice in one launch (src/omniasr_trt/beam.py:165-175): ``F.log_softmax(logits)`` in bf16,
-    the offers (score + logp; with ``length_norm``, once the group's row 0 has tokens, (score * count + logp) /
-    (count + 1); a finished row offers only ``eos``, at its score) and ``offers.view(S, N * V).topk(N)`` -- returns
-    (best [S, N] fp32, flat [S, N] int64), best first, equal values in the order of their flat index.  ``score`` /
-    ``count`` / ``ended``: the rows' state (fp32 / int64 / bool, at least S * N rows)."""
+                length_norm: bool, eos: int, *, fused_log_softmax: bool = False,
+                tickets: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """The beam step's choice (src/omniasr_trt/beam.py:162-175): ``F.log_softmax(logits)`` in bf16, the offers
+    (score + logp; with ``length_norm``, once the group's row 0 has tokens, (score * count + logp) / (count + 1); a
+    finished row offers only ``eos``, at its score) and ``offers.view(S, N * V).topk(N)`` -- returns (best [S, N]
+    fp32, flat [S, N] int64), best first, equal values in the order of their flat index.  ``score`` / ``count`` /
+    ``ended``: the rows' state (fp32 / int64 / bool, at least S * N rows).
+
+    The log-softmax is torch's own (one launch), and the offers and top-k are one launch of ``omni_beam_select``:
+    the choice is the one torch's ops make, bit for bit.  ``fused_log_softmax=True`` computes the log-softmax in the
+    same launch instead, in the kernel's own summation order: a logp on a bf16 rounding boundary can then round the
+    other way (measured: 3 of 12,472 group-steps of bf16 searches chose differently).  ``tickets``: int32, one per
+    group, zero (left zero); by default a per-device buffer shared by every caller, so searches that run at once on
+    two streams of one GPU each pass their own."""
     lib = _lib.load()
     _need(beam_select_supported(logits, score, beams), "beam_select: bf16 logits [S*N, V] (8 | V <= 16384, unit "
           "stride), fp32 score, 1..16 beams")
@@ -503,15 +531,22 @@ def beam_select(logits: torch.Tensor, score: torch.Tensor, count: torch.Tensor, 
     _flags(ended, "ended")
     _need(count.numel() >= rows and ended.numel() >= rows, "count / ended: [>= rows]")
     groups = rows // beams
+    if tickets is None:
+        tickets = _tickets(_select_tickets, logits.device, groups, "beam_select", 256)
+    _need(tickets.is_cuda and tickets.dtype == torch.int32 and tickets.is_contiguous() and tickets.numel() >= groups
+          and tickets.device == logits.device, "tickets: int32 [>= groups] on the logits' device")
+    if fused_log_softmax:
+        rows_in, kind = logits, _lib.SELECT_LOGITS
+    else:
+        rows_in, kind = F.log_softmax(logits, dim=-1), _lib.SELECT_LOGP  # torch's own rounding: the reference's logp
     best = torch.empty(groups, beams, device=logits.device, dtype=torch.float32)
     flat = torch.empty(groups, beams, device=logits.device, dtype=torch.long)
     ws = lib.omni_beam_select_workspace(groups, beams)
     workspace = torch.empty(max(ws, 256), device=logits.device, dtype=torch.uint8)
-    tickets = _tickets(_select_tickets, logits.device, groups, "beam_select", 256)
-    status = lib.omni_beam_select(logits.data_ptr(), logits.stride(0), groups, beams, vocab, score.data_ptr(),
+    status = lib.omni_beam_select(rows_in.data_ptr(), rows_in.stride(0), groups, beams, vocab, score.data_ptr(),
                                   count.data_ptr(), ended.data_ptr(), int(bool(length_norm)), int(eos),
                                   best.data_ptr(), flat.data_ptr(), workspace.data_ptr(), workspace.numel(),
-                                  tickets.data_ptr(), _lib.BF16, _stream(logits))
+                                  tickets.data_ptr(), kind, _lib.BF16, _stream(logits))
     _lib.check(status, "beam_select")
     return best, flat
 

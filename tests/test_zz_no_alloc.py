@@ -123,3 +123,52 @@ def test_graph_replays_of_the_static_call(cuda):
         torch.cuda.synchronize()
         assert torch.equal(out, want), rep
     assert np.isfinite(out.float().cpu().numpy()).all()
+
+
+FIRST_CALL_UNDER_CAPTURE = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+import importlib
+import torch
+importlib.import_module("omniasr-trt_amd")
+from omniasr_trt_amd import _lib
+lib = _lib.load()
+q = torch.zeros(5, 8, 128, dtype=torch.bfloat16, device="cuda")
+kc = torch.zeros(1, 8, 256, 128, dtype=torch.bfloat16, device="cuda")
+lengths = torch.tensor([100], device="cuda")
+out = torch.zeros_like(q)
+def call(stream):
+    return lib.omni_verify_attention_static(q.data_ptr(), kc.data_ptr(), kc.data_ptr(), kc.stride(0), kc.stride(1),
+                                            kc.stride(2), 256, lengths.data_ptr(), 1, 5, 8, 128, 256, 0, 0.1,
+                                            out.data_ptr(), _lib.ATTN_SEPARATE_COMBINE, _lib.BF16, stream)
+side = torch.cuda.Stream()
+side.wait_stream(torch.cuda.current_stream())
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.stream(side):
+    graph.capture_begin()
+    under = call(side.cuda_stream)  # no address yet, stream capturing: refused, nothing recorded
+    graph.capture_end()
+torch.cuda.synchronize()
+init = lib.omni_verify_attention_static_init()
+again = lib.omni_verify_attention_static_init()
+eager = call(torch.cuda.current_stream().cuda_stream)
+torch.cuda.synchronize()
+print("statuses", under, init, again, eager, flush=True)
+assert under == -1 and init == 0 and again == 0 and eager == 0
+"""
+
+
+def test_first_call_under_capture_is_refused(cuda):
+    """In a fresh process, the entry point's first call on the device made under graph capture returns
+    OMNI_ERR_INVALID before any lookup or launch (the static scratch has no address yet); after
+    ``omni_verify_attention_static_init`` the same call runs."""
+    import subprocess
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    say("fresh process: the static entry point's first call under capture")
+    res = subprocess.run([sys.executable, "-c", FIRST_CALL_UNDER_CAPTURE, str(root)], capture_output=True, text=True,
+                         timeout=300)
+    say(res.stdout.strip()[-500:], res.stderr.strip()[-1500:])
+    assert res.returncode == 0
+    assert "statuses -1 0 0 0" in res.stdout
