@@ -335,8 +335,9 @@ def time_small_kernels(pkg, torch, dec, reps: int = 200) -> dict:
         us, tus = timed(ours, reps), timed(theirs, reps)
         res[name] = {"us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1),
                      "torch_us": round(tus, 2)}
-    # The beam step's choice at config 5b's size (8 inputs x 5 beams): one launch against torch's log-softmax, the
-    # offers' element-wise ops and topk.
+    # The beam step's choice at config 5b's size (8 inputs x 5 beams): torch's log-softmax and one launch (the
+    # default, the reference's choice bit for bit), the log-softmax fused into that launch, and torch's log-softmax,
+    # the offers' element-wise ops and topk.
     n, rows, vocab = BEAMS, SLOTS * BEAMS, cfg.vocab_size
     lg = torch.randn(rows, vocab, device="cuda", generator=g).mul_(4).to(torch.bfloat16)
     sc = -torch.rand(rows, device="cuda", generator=g) * 30
@@ -353,8 +354,9 @@ def time_small_kernels(pkg, torch, dec, reps: int = 200) -> dict:
         return off.view(SLOTS, n * vocab).topk(n, dim=-1, sorted=True)
 
     us = timed(lambda: kernels.beam_select(lg, sc, ct, en, n, True, 2), reps)
-    res[f"beam_select_{SLOTS}x{n}x{vocab}"] = {"us": round(us, 2), "bytes": lg.numel() * 2,
-                                                "torch_us": round(timed(torch_select, reps), 2)}
+    fused = timed(lambda: kernels.beam_select(lg, sc, ct, en, n, True, 2, fused_log_softmax=True), reps)
+    res[f"beam_select_{SLOTS}x{n}x{vocab}"] = {"us": round(us, 2), "fused_log_softmax_us": round(fused, 2),
+                                                "bytes": lg.numel() * 2, "torch_us": round(timed(torch_select, reps), 2)}
     return res
 
 
@@ -610,9 +612,94 @@ def host_cpu() -> tuple[int, str]:
     return cores, model
 
 
+def _median_call(fn, reps: int, budget: float) -> tuple[float, int]:
+    """Seconds per call of ``fn``: 1 warm-up call, then the median of at least ``reps`` timed calls (more while
+    ``budget`` seconds last)."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget
+    while len(times) < reps or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 4 * reps:
+            break
+    return float(np.median(times)), len(times)
+
+
+def cpu_configs(pkg, budget: float = 2.0) -> dict:
+    """Configs 1-3 on the host cores, per call, with the oracle's numpy kernels (the fp64 attention, the fp32
+    log-softmax argmax, the acceptance loop, the RoPE + append): seeded inputs of each config's shape (seed 1000 +
+    config), 1 warm-up call, then the median of >= 5 calls."""
+    from oracle import verify as ov
+
+    res = {}
+    heads, dim, vocab = 32, 128, 10288
+    scale = dim ** -0.5
+    eos, limit = pkg.llm.EOS, pkg.decode.LIMIT
+
+    def bf16(a):
+        return ov.round_to(np.asarray(a, np.float32), "bf16")
+
+    # Config 1: one slot, 1 + 4 queries over 1024 prior keys, then greedy acceptance over [5, V] bf16 logits with a
+    # planted argmax matching the first 2 drafts.
+    rng = np.random.default_rng(1001)
+    t1, n1 = DRAFT + 1, 1024
+    q = bf16(rng.standard_normal((t1, heads, dim)))
+    kc = bf16(rng.standard_normal((1, heads, n1 + t1, dim)))
+    vc = bf16(rng.standard_normal((1, heads, n1 + t1, dim)))
+    logits = bf16(rng.standard_normal((t1, vocab)))
+    tokens = rng.integers(3, vocab, (1, t1))
+    logits[0, tokens[0, 1]] = logits[1, tokens[0, 2]] = 8.0
+    lens1 = np.array([n1])
+
+    def config1():
+        ov.verify_attention(q, kc, vc, lens1, t1, scale)
+        nxt = ov.log_softmax_argmax(logits).reshape(1, t1)
+        out = np.zeros((1, 4096), np.int32)
+        ov.accept(tokens, nxt, out, np.zeros(1, np.int64), np.array([n1 - 1]), np.zeros(1, bool), None, None, None,
+                  limit, eos)
+
+    sec, n = _median_call(config1, 5, budget)
+    res["config1_verify_step"] = {"ms_per_call": round(sec * 1e3, 3), "calls": n,
+                                  "sample": "attention B=1 T=5 32x128 over 1024 keys (fp64) + log-softmax argmax of "
+                                            "[5, 10288] + acceptance"}
+    # Config 2: RoPE + KV append, 8 slots x 5 tokens, 32 heads x 128, capacity 4096, positions = lengths U[200, 2000].
+    rng = np.random.default_rng(1002)
+    cap = 4096
+    qkv = bf16(rng.standard_normal((SLOTS * t1, 3 * heads * dim)))
+    base = rng.integers(200, 2001, SLOTS)
+    pos = (base[:, None] + np.arange(t1)).reshape(-1)
+    slots = np.repeat(np.arange(SLOTS), t1)
+    cs = ov.rope_table(dim, cap)
+    kc2 = np.zeros((SLOTS, heads, cap, dim), np.float32)
+    vc2 = np.zeros_like(kc2)
+    sec, n = _median_call(lambda: ov.rope_kv(qkv, cs, pos, kc2, vc2, heads, slots), 5, budget)
+    res["config2_rope_kv"] = {"ms_per_call": round(sec * 1e3, 3), "calls": n,
+                              "sample": "8 slots x 5 tokens, 32 x 128, capacity 4096"}
+    del kc2, vc2
+    # Config 3: 8 rows, T = 5, lengths U[750, 2400] (the GPU leg's lengths), fp64 attention.
+    rng = np.random.default_rng(1003)
+    lengths = rng.integers(750, 2401, SLOTS)
+    keys = -(-(int(lengths.max()) + t1) // 256) * 256
+    q3 = bf16(rng.standard_normal((SLOTS * t1, heads, dim)))
+    # One row's worth of keys and values shared by the 8 rows (the oracle converts each row's keys on its own, so the
+    # time is a fresh row's; generating 8 distinct rows would only lengthen the set-up).
+    kc3 = np.broadcast_to(rng.standard_normal((1, heads, keys, dim), dtype=np.float32), (SLOTS, heads, keys, dim))
+    vc3 = np.broadcast_to(rng.standard_normal((1, heads, keys, dim), dtype=np.float32), (SLOTS, heads, keys, dim))
+    sec, n = _median_call(lambda: ov.verify_attention(q3, kc3, vc3, lengths, t1, scale), 5, budget)
+    nbytes = attention_bytes(lengths, t1, heads, dim)
+    res["config3_verify_attention"] = {"ms_per_call": round(sec * 1e3, 3), "calls": n,
+                                       "GBps_algorithmic": round(nbytes / sec / 1e9, 2),
+                                       "sample": "8 rows x 5 queries, 32 x 128, lengths U[750, 2400] (fp64; "
+                                                 "N(0, 1) values, one row's keys shared by the rows)"}
+    return res
+
+
 def cpu_baseline(pkg, torch, w: Workload, seconds: float) -> dict:
-    """The numpy oracle's drafted step (fp32) on the host from the same post-prefill state, for about ``seconds``,
-    its BLAS on every core this process may use."""
+    """The numpy oracle's drafted step (fp32) on the host from the same post-prefill state: 1 warm-up step, then
+    timed steps for about ``seconds`` (at least 5), its BLAS on every core this process may use; plus configs 1-3
+    per call (:func:`cpu_configs`)."""
     from threadpoolctl import threadpool_limits
 
     from oracle import step as ostep
@@ -630,20 +717,30 @@ def cpu_baseline(pkg, torch, w: Workload, seconds: float) -> dict:
                                    v, state, DRAFT, spec.NGRAM, spec.BEHIND, spec.AHEAD, spec.REACH, spec.SELF_WINDOW,
                                    spec.SELF_MIN, pkg.decode.LIMIT, pkg.llm.EOS)
     cores, model = host_cpu()
-    tokens = steps = 0
-    with threadpool_limits(limits=cores, user_api="blas"):
+
+    def one_step() -> tuple[int, float]:
+        need = int(state["last"].max()) + 8 * (DRAFT + 1) + 2
+        keys = min(cap, -(-need // 256) * 256)
         t0 = time.perf_counter()
-        while time.perf_counter() - t0 < seconds:
-            need = int(state["last"].max()) + 8 * (DRAFT + 1) + 2
-            keys = min(cap, -(-need // 256) * 256)
-            tokens += npdec.step(keys)
-            steps += 1
-        elapsed = time.perf_counter() - t0
+        got = npdec.step(keys)
+        return got, time.perf_counter() - t0
+
+    tokens, times = 0, []
+    with threadpool_limits(limits=cores, user_api="blas"):
+        one_step()  # warm-up
+        t_end = time.perf_counter() + seconds
+        while len(times) < 5 or time.perf_counter() < t_end:
+            got, dt = one_step()
+            tokens += got
+            times.append(dt)
+        configs = cpu_configs(pkg)
+    elapsed = float(np.sum(times))
     return {"value": round(tokens / elapsed, 2), "unit": "verified tokens/s", "cores": cores,
-            "kind": "port", "sample": f"{steps} drafted steps of config 4 (8 slots x 5 tokens, 12 layers, fp32 numpy "
-                                      f"oracle, tests/test_oracle_step.py pins it) from the post-prefill state, "
-                                      f"{elapsed:.1f} s, {tokens} tokens",
-            "cpu": model}
+            "kind": "port", "median_step_s": round(float(np.median(times)), 4),
+            "sample": f"1 warm-up + {len(times)} drafted steps of config 4 (8 slots x 5 tokens, 12 layers, fp32 numpy "
+                      f"oracle, tests/test_oracle_step.py pins it) from the post-prefill state, {elapsed:.1f} s, "
+                      f"{tokens} tokens",
+            "cpu": model, "configs": configs}
 
 
 def main() -> int:
@@ -807,7 +904,9 @@ def main() -> int:
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "kernel": "verify_attn_pair_kernel<128> (config 3, T = 5)",
                      "achieved": attn["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": attn["frac_peak"],
-                     "traffic": measured_traffic(), "bytes_per_launch": attn["bytes"], "us_per_launch": attn["us"]},
+                     "traffic": measured_traffic(), "bytes_per_launch": attn["bytes"], "us_per_launch": attn["us"],
+                     "traffic_source": "the committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary of this launch "
+                                       "(profiles/verify_attention_config3.md), not measured in this run"},
         "cpu_baseline": cpu,
         "ctc_drafts": ctc,
         "beam_search": beams,

@@ -2,8 +2,11 @@
 //   rms_norm   y = x * rsqrt(mean(x^2) + eps) * w per row (F.rms_norm, src/omniasr_trt/modeling.py's RMSNorm);
 //   silu_mul   out = inner * silu(gate) for the fused gate|inner projection's halves (decode.py:34-54's layout,
 //              the FFN of SpecDecoder.step, src/omniasr_trt/spec.py:97-106).
-// bf16 in and out, fp32 arithmetic.  rms_norm rounds once, after both products (torch's fused kernel does the same);
-// silu_mul rounds silu(gate) to bf16 and then the product, as torch's two kernels do.  At step sizes ([40, 4096],
+// bf16 in and out, fp32 arithmetic.  rms_norm rounds once, after both products, as F.rms_norm does, but adds the
+// row's squares in its own order (fused multiply-adds per thread, then a wave and workgroup reduction): where that
+// sum differs from torch's in its last bit, rsqrt can too, and an output can round to the neighbouring bf16 value
+// (measured: ~3 of 10^6 elements); silu_mul rounds silu(gate) to bf16 and then the product, as torch's two kernels
+// do, bit for bit.  At step sizes ([40, 4096],
 // [40, 2 x 11008]) both are a few hundred KB, so they are latency-bound: one workgroup per row for the norm (the
 // row's sum of squares in registers, one LDS reduction), one thread per 8 outputs for silu_mul.
 #include <math.h>

@@ -165,11 +165,16 @@ class Transcriber:
         return [self.text(r) for r in rows]
 
     @torch.inference_mode()
-    def transcribe(self, audio: list, langs=None, *, beams: int | None = None, length_norm: bool | None = None,
-                   drafts=None) -> list:
+    def transcribe(self, audio: list, langs=None, *, mode: str = "fast", beams: int | None = None,
+                   length_norm: bool | None = None, drafts=None) -> list:
         """Token ids (or texts, with a tokenizer) of each input.  ``beams`` / ``length_norm``: the search (default: the
         transcriber's).  ``drafts``: per input the CTC argmax of each 20 ms frame (default: the drafter's, if any),
-        used by the greedy search only.  (src/omniasr_trt/llm.py:255-282)"""
+        used by the greedy search only.  ``mode``: "fast" (the batched decoders on the MI355X kernels); the
+        reference's "reference" mode -- its batch-1 torch loops -- is not a path of this package and is refused.
+        (src/omniasr_trt/llm.py:255-282)"""
+        if mode != "fast":
+            raise ValueError(f"mode={mode!r}: only 'fast' (the batched MI355X decoders); the reference's batch-1 "
+                             "'reference' loops are not part of this package")
         beams = self.beams if beams is None else beams
         length_norm = self.length_norm if length_norm is None else length_norm
         greedy = beams == 1 and not length_norm

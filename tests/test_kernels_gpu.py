@@ -118,6 +118,40 @@ def test_verify_attention_bf16(cuda, t):
     _attn_case(cuda, torch.bfloat16, 4, 4, 256, t, 700, lengths, 640, 5, BF16_TOL)  # two 128-dimension slices
 
 
+@pytest.mark.parametrize("dtype,rows,heads,d", [(torch.bfloat16, 8, 32, 128), (torch.bfloat16, 3, 4, 128),
+                                                 (torch.bfloat16, 8, 8, 512), (torch.float32, 5, 4, 64),
+                                                 (torch.float32, 4, 2, 512)])
+def test_decode_attention_shim(cuda, dtype, rows, heads, d):
+    """``kernels.decode_attention`` through its own signature, as the reference's one-token step calls it
+    (src/omniasr_trt/decode.py:203-204: ``decode_attention(q, self.k[i], self.v[i], lengths, keys, scale)`` on a
+    layer's [max_batch, H, S, D] cache, q [B, H, D]), and with the reference's Triton settings passed explicitly
+    (accepted and ignored) and a ``chunk`` override: against the oracle's attention at one query per row, a row of
+    length 0 giving zeros (src/omniasr_trt/kernels.py:210)."""
+    g = gen(rows * 100 + heads + d)
+    cap, max_batch = 1536, rows + 3
+    layers_k = torch.randn(2, max_batch, heads, cap, d, generator=g).to(dtype)
+    layers_v = torch.randn(2, max_batch, heads, cap, d, generator=g).to(dtype)
+    lengths = torch.randint(1, 1400, (rows,), generator=g)
+    lengths[rows // 2] = 0
+    lengths[0] = 1
+    keys = -(-int(lengths.max()) // 256) * 256
+    q = torch.randn(rows, heads, d, generator=g).to(dtype)
+    kd, vd, qd, ld = layers_k.to(cuda), layers_v.to(cuda), q.to(cuda), lengths.to(cuda)
+    want = ov.verify_attention(npf(q), npf(layers_k[1]), npf(layers_v[1]), lengths.numpy(), 1, d ** -0.5)
+    tol = BF16_TOL if dtype == torch.bfloat16 else F32_TOL
+    outs = []
+    for kw in ({}, {"block": 64, "warps": 8, "stages": 2, "programs": 264}, {"chunk": 256}):
+        say(f"decode_attention dtype={dtype} rows={rows} heads={heads} d={d} keys={keys} {kw}")
+        out = kernels.decode_attention(qd, kd[1], vd[1], ld, keys, d ** -0.5, **kw)
+        torch.cuda.synchronize()
+        assert out.shape == q.shape and out.dtype == dtype
+        np.testing.assert_allclose(npf(out), want, atol=tol[0], rtol=tol[1])
+        assert not npf(out[rows // 2]).any()  # the empty row: zeros
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])  # the Triton settings change nothing
+    assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
+
+
 @pytest.mark.parametrize("t,d", [(20, 512), (32, 512), (32, 256)])
 def test_verify_attention_wide_heads_up_to_32_queries(cuda, t, d):
     """Head dims 256 / 512 take up to 32 queries per row (two 16-query groups per wave): against the oracle, both

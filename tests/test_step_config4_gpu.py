@@ -11,9 +11,11 @@ drafted steps, with every kernel's inputs recorded and its effect checked agains
   equals ``oracle.verify.accept`` applied to the state before: the kept tokens are the argmaxes of the step's own
   logits, and every running slot advances by n + 1 in [1, 5] positions.
 
-Two phases of STEPS steps each: own-token drafting from the seeded history (the benchmark's main leg; the random
-model's argmax rarely follows a repeat, so about one token per step), then perfect drafts -- the run's own greedy
-tokens as CTC frames, loaded through ``Row.draft`` and ``SpecDecoder.filled`` -- where most proposals are kept.
+Three phases of STEPS steps each, every one from the post-prefill state: own-token drafting from the seeded history
+(the benchmark's main leg; the random model's argmax rarely follows a repeat, so about one token per step); perfect
+drafts -- the run's own greedy tokens as CTC frames, loaded through ``Row.draft`` and ``SpecDecoder.filled`` -- where
+most proposals are kept; and config 5a's drafts, the same frames with 10% of their tokens substituted, where a
+proposal is kept up to its first substituted token.  The frames carry enough tokens for every checked step.
 
 The decoder layer math between the kernels (GEMMs, norms) is torch's; what is checked here is the kernels at the
 shapes the benchmark times, inside the decoder, with the state they really see."""
@@ -79,10 +81,14 @@ def test_config4_drafted_steps(cuda, monkeypatch):
 
     with torch.inference_mode():
         # perfect drafts for the second phase: the run's own greedy tokens, as CTC frames through Row.draft -> filled
-        conts = w.greedy_continuations(3 * STEPS)
+        conts = w.greedy_continuations(8 * STEPS)
         per_segment = pkg.llm.SEGMENT // pkg.llm.HOP
         frames = [pkg.transcribe.frames_from_tokens([c], per_segment, np.random.default_rng(i))
                   for i, c in enumerate(conts)]
+        noisy = [pkg.transcribe.frames_from_tokens([c], per_segment, np.random.default_rng(100 + i), substitute=0.1,
+                                                   vocab=w.cfg.vocab_size) for i, c in enumerate(conts)]
+    say(f"continuation lengths {[len(c) for c in conts]} (a step keeps at most {bench.DRAFT + 1} tokens)")
+    assert min(len(c) for c in conts) >= (bench.DRAFT + 1) * STEPS + 1
     monkeypatch.setattr(kernels, "spec_prepare", prepare)
     monkeypatch.setattr(kernels, "rope_kv", rope)
     monkeypatch.setattr(kernels, "greedy_accept", accept)
@@ -90,9 +96,9 @@ def test_config4_drafted_steps(cuda, monkeypatch):
     fragile_rows = 0
     accepted = {}
     with torch.inference_mode():
-        for phase in ("own tokens", "frame drafts"):
-            if phase == "frame drafts":
-                w.load_frame_drafts(frames)
+        for phase in ("own tokens", "frame drafts", "substituted frame drafts"):
+            if phase != "own tokens":
+                w.load_frame_drafts(frames if phase == "frame drafts" else noisy)
             accepted[phase] = 0
             for step in range(STEPS):
                 before = {name: host(getattr(dec, name)[:b]) for name in
@@ -153,8 +159,10 @@ def test_config4_drafted_steps(cuda, monkeypatch):
                 assert ((advance[running] >= 1) & (advance[running] <= bench.DRAFT + 1)).all(), advance
                 accepted[phase] += int(advance[running].sum())
                 say(f"{phase}, step {step}: accepted {advance.tolist()}")
-    rows_checked = 2 * STEPS * b * (bench.DRAFT + 1)
-    say(f"config 4: {2 * STEPS} steps checked; {fragile_rows} of {rows_checked} argmax rows lse-fragile; tokens accepted "
+    rows_checked = 3 * STEPS * b * (bench.DRAFT + 1)
+    say(f"config 4: {3 * STEPS} steps checked; {fragile_rows} of {rows_checked} argmax rows lse-fragile; tokens accepted "
         f"{accepted}")
-    # the greedy run's own tokens as drafts: most proposals are kept (several tokens per row-step)
+    # the greedy run's own tokens as drafts: most proposals are kept (several tokens per row-step); with 10% of them
+    # substituted, fewer but still more than one per row-step
     assert accepted["frame drafts"] > 2 * STEPS * b
+    assert accepted["substituted frame drafts"] > 1.5 * STEPS * b

@@ -104,7 +104,9 @@ def test_frame_drafts_through_the_transcriber(case, monkeypatch):
     say(f"transcriber: {per_step:.2f} tokens per row-step with clean drafts")
     assert per_step > 1.5
     say("transcriber: CTC-like drafts (10% substitutions), some inputs without frames")
-    assert t.transcribe(inputs, langs, drafts=noisy) == want
+    assert t.transcribe(inputs, langs, mode="fast", drafts=noisy) == want  # the reference's keyword and default
+    with pytest.raises(ValueError, match="reference"):
+        t.transcribe(inputs, langs, mode="reference")  # the reference's batch-1 loops are not part of this package
     assert t.transcribe(inputs, langs, drafts=[None, noisy[1], None, clean[3], None]) == want
     say("transcriber: a drafter object, then own tokens only")
     t.drafter = FakeDrafter(noisy)
