@@ -365,6 +365,48 @@ def test_verify_attention_graph_replays(cuda, split_k):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("h,d", [(32, 128), (8, 512)])
+def test_verify_attention_merge_under_load(cuda, h, d):
+    """The in-kernel merges (the halves kernel's tickets at 8 x 32 x 128, the balanced wide-head kernel's at
+    8 x 8 x 512) under sustained concurrent load: 96 launches queued back to back on each of two streams -- the
+    workspace entry point on one, the static-scratch entry point on the other, so each merge shares its CUs, L2 and
+    HBM with the other stream's waves -- over 8 sets of ragged lengths (empty and one-key rows among them).  Every
+    launch equals the first eager result for its lengths bit for bit (a partial read before its writer's stores
+    landed would change the bits; a ticket left non-zero would break the next launch's merge), those results match
+    the oracle, and the workspace path's tickets are left zero."""
+    g = gen(70 + d)
+    b, t, cap, reps = 8, 5, 2560, 96
+    kc = torch.randn(b, h, cap, d, generator=g).to(torch.bfloat16)
+    vc = torch.randn(b, h, cap, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(b * t, h, d, generator=g).to(torch.bfloat16)
+    sets = [torch.randint(750, 2401, (b,), generator=g) for _ in range(8)]
+    sets[1][2], sets[3][0], sets[5][7] = 0, 1, 0
+    kd, vd, qd = kc.to(cuda), vc.to(cuda), q.to(cuda)
+    lens = [s.to(cuda) for s in sets]
+    first = [kernels.draft_attention(qd, kd, vd, ln, t, cap, d ** -0.5) for ln in lens]
+    torch.cuda.synchronize()
+    for j in (0, 1):  # the oracle on two of the sets (the rest are checked through the first results' bits)
+        want = ov.verify_attention(npf(q), npf(kc), npf(vc), sets[j].numpy(), t, d ** -0.5)
+        np.testing.assert_allclose(npf(first[j]), want, atol=BF16_TOL[0], rtol=BF16_TOL[1])
+    outs_a, outs_b = [], []
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    sa.wait_stream(torch.cuda.current_stream())
+    sb.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(sb):
+        outs_b = [torch.empty_like(qd) for _ in range(reps)]
+    say(f"merge under load: h={h} d={d}, {reps} launches on each of two streams")
+    for i in range(reps):
+        with torch.cuda.stream(sa):
+            outs_a.append(kernels.draft_attention(qd, kd, vd, lens[i % 8], t, cap, d ** -0.5))
+        with torch.cuda.stream(sb):
+            kernels.verify_attention_static(qd, kd, vd, lens[(i + 3) % 8], t, cap, d ** -0.5, outs_b[i])
+    torch.cuda.synchronize()
+    for i in range(reps):
+        assert torch.equal(outs_a[i], first[i % 8]), f"workspace entry point, launch {i}"
+        assert torch.equal(outs_b[i], first[(i + 3) % 8]), f"static entry point, launch {i}"
+    assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
+
+
 # ---------------------------------------------------------------------------------------------- argmax + accept
 
 def _done_state(cuda, b, t, cap=64):
