@@ -66,6 +66,27 @@ __device__ __forceinline__ void load_tile_clamped(KVTile<D>& t, const char* kt, 
   }
 }
 
+// A tile of 32 gathered key rows into MFMA operand layout: ``rows`` (in LDS) holds the byte offset of each of the
+// tile's 32 keys from ``kt`` / ``vt`` (the same offset in K and V); every offset is a key in use.
+template <int D>
+__device__ __forceinline__ void load_tile_rows(KVTile<D>& t, const char* kt, const char* vt, const uint32_t* rows, int c,
+                                               int g) {
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+    const uint32_t ko = rows[8 * (c >> 2) + 4 * mb + (c & 3)] + g * 16;
+#pragma unroll
+    for (int s = 0; s < KVTile<D>::KS; ++s) t.k[mb][s] = ld16(kt + ko + s * 64);
+  }
+  const u32x4_t r0 = *reinterpret_cast<const u32x4_t*>(rows + 8 * g);
+  const u32x4_t r1 = *reinterpret_cast<const u32x4_t*>(rows + 8 * g + 4);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t vo = (j < 4 ? r0[j] : r1[j - 4]) + c * 16;
+#pragma unroll
+    for (int gg = 0; gg < KVTile<D>::NG; ++gg) t.v[gg][j] = ld16(vt + vo + gg * 256);
+  }
+}
+
 // S^T for the tile: lane (c, g) gets query c's raw scores for keys kb + 8g + j, j = 0..7.
 template <int D>
 __device__ __forceinline__ void tile_scores(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float (&sv)[8]) {
@@ -132,14 +153,15 @@ struct SoftmaxState {
 
 // A tile with its raw scores ``sv`` (lane (c, g): query c, keys key0 + j): the causal / end-of-row mask (key0 + j >=
 // lim: query c does not see key j of this lane), the lazy reference max, probabilities, O += P V.  The mask is a no-op
-// on tiles every query sees whole.
-template <int D>
+// on tiles every query sees whole.  kRange: the mask is 0 <= key0 + j < lim (keys numbered from a range's start).
+template <int D, bool kRange = false>
 __device__ __forceinline__ void attend_scored(const KVTile<D>& t, float (&sv)[8], float c_scale, SoftmaxState& st,
                                               f32x4_t (&o)[D / 16], int g, int key0, int lim) {
   bool over = false;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    sv[j] = key0 + j < lim ? sv[j] : -INFINITY;
+    const bool seen = kRange ? (uint32_t)(key0 + j) < (uint32_t)lim : key0 + j < lim;
+    sv[j] = seen ? sv[j] : -INFINITY;
     over |= sv[j] > st.thr;
   }
   if (__any(over)) {
@@ -170,6 +192,18 @@ __device__ __forceinline__ void attend(const KVTile<D>& t, const u32x4_t (&qop)[
   float sv[8];
   tile_scores<D>(t, qop, sv);
   attend_scored<D>(t, sv, c_scale, st, o, g, key0, lim);
+}
+
+// One tile whose keys query c sees form the range [lo, lim) of the tile's numbering (key0 + j for this lane's keys):
+// a range that starts at 0 is attend's mask; a range inside a list of several queries' keys selects query c's own.
+template <int D>
+__device__ __forceinline__ void attend_range(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float c_scale,
+                                             SoftmaxState& st, f32x4_t (&o)[D / 16], int g, int key0, int lo,
+                                             int lim) {
+  float sv[8];
+  tile_scores<D>(t, qop, sv);
+  // key0 + j in [lo, lim): the keys renumbered from lo, then one unsigned compare
+  attend_scored<D, true>(t, sv, c_scale, st, o, g, key0 - lo, lim > lo ? lim - lo : 0);
 }
 
 // A workgroup barrier ordering LDS accesses only: global loads in flight stay in flight across it (a full

@@ -56,6 +56,16 @@ struct AttnArgs {
   int gen_split;     // partial slot of the beams' generated keys (merged with the key splits), or -1
   int balanced;      // wide-head split-K with a fixed number of workgroups per head (see balanced_split)
   int rows;          // rows of the launch (balanced split-K)
+  // The beams' generated keys as tiles of the halves kernel (verify_attn_pair_kernel<D, true>): key j of row r (the
+  // unit's group g = r / T, beam r - g T) is position j of generated-cache row ptr[r, j], j < gen_len[r] <= gen_cap.
+  const char* kg = nullptr;  // generated K / V, [gen_rows, H, gen_cap, D] with key rows of D elements
+  const char* vg = nullptr;
+  int64_t g_row = 0, g_head = 0;  // element strides of a generated-cache row and head
+  const int32_t* ptr = nullptr;
+  int64_t ptr_stride = 0;
+  const int64_t* gen_len = nullptr;
+  int gen_cap = 0, gen_rows = 0;
+  int gen_table = 0;  // LDS entries of a unit's table of generated-key offsets (a multiple of 32)
 };
 
 struct SplitRange {
@@ -691,6 +701,8 @@ constexpr int kWgMaxT = 11;  // the waves' states, the fetched partials and the 
 constexpr int64_t kWgMinUnits = 128;  // rows x heads from which one workgroup per (head, row) beats split-K
 
 constexpr int kPairMaxRows = 256;
+constexpr int64_t kPairMaxGenTable = 4096;  // generated keys of a unit taken as tiles of the halves kernel
+constexpr size_t kPairMaxLds = 64 * 1024;   // dynamic LDS of the halves kernel
 constexpr int64_t kPairMaxQueryRows = int64_t{1} << 30;  // query rows x heads: 32-bit row indices in the kernel
 
 // The row's tile count: 32-key tiles up to the keys its last query sees.
@@ -791,9 +803,16 @@ __device__ __forceinline__ PartialItem merge_slots(const float* po, const float*
 // ticket to zero.
 constexpr int kTicketFirst = 1, kTicketClaim = 2, kTicketSecond = 4;
 
-// Dynamic LDS of the halves kernel: the waves' states, the two fetched partials of unit 1, half 1's queries (bf16).
-__host__ __device__ constexpr size_t pair_lds_bytes(int T, int D) {
-  return (size_t)(kWgWaves + 2) * T * (D + 2) * sizeof(float) + (size_t)T * D * 2;
+// Dynamic LDS of the halves kernel: the waves' states, the two fetched partials of unit 1, half 1's queries (bf16);
+// with generated keys (beams) also every row's generated-key count and the two units' tables of key offsets.
+__host__ __device__ constexpr size_t pair_lds_bytes(int T, int D, int rows = 0, int gen_table = 0) {
+  return (size_t)(kWgWaves + 2) * T * (D + 2) * sizeof(float) + (size_t)T * D * 2 +
+         (((size_t)rows * T + 3) / 4 * 4 + 2 * (size_t)gen_table) * sizeof(int32_t);
+}
+
+// The generated keys of row ``row`` (a beam) in use.
+__device__ __forceinline__ int gen_count(const AttnArgs& a, int64_t row) {
+  return (int)clamp64(a.gen_len[row], 0, a.gen_cap);
 }
 
 // One 8-wave workgroup per (head, row) unit, working on halves: units are ranked by length, and workgroup i takes
@@ -807,7 +826,12 @@ __host__ __device__ constexpr size_t pair_lds_bytes(int T, int D) {
 // next tiles load.  The first wave to finish half 1 claims unit 1 (see kTicketFirst) and, if its first half is out,
 // fetches it into LDS while the other waves finish, so the common end is an LDS merge and the output store.  The
 // dealing is static, so results do not depend on timing.
-template <int D>
+//
+// GEN (beams): each unit's tiles are its context tiles followed by its beams' generated keys -- beam 0's, then beam
+// 1's, ... as one list cut into 32-key tiles, key f at the byte offset the workgroup's table in LDS gives (row
+// ptr[r, j] of the generated cache, position j) -- and query (beam) i sees only its own run [P_i, P_i+1) of that list,
+// so the halves deal, the pipeline and the merges treat the generated keys like any other tile.
+template <int D, bool GEN = false>
 __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(AttnArgs a, int rows, int slots) {
   static_assert(D == 128, "the halves kernel serves head dim 128");
   constexpr int KS = D / 32;
@@ -821,8 +845,23 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
   const int tid = threadIdx.x, lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int T = a.T, H = a.H, U = rows * H;
+  // GEN: every row's generated-key counts [rows][T], then the two units' offset tables, after half 1's queries
+  int* s_gl = reinterpret_cast<int*>(smem + (kWgWaves + 2) * T * (D + 2) + T * D / 2);
+  uint32_t* tab = reinterpret_cast<uint32_t*>(s_gl + ((rows * T + 3) & ~3));  // 16-byte aligned (row reads)
   if (tid == 0) s_done = 0;
-  for (int b = tid; b < rows; b += 64 * kWgWaves) ntl[b] = row_tile_count(a, b);
+  for (int b = tid; b < rows; b += 64 * kWgWaves) {
+    int nt = row_tile_count(a, b);
+    if constexpr (GEN) {
+      int ng = 0;
+      for (int e = 0; e < T; ++e) {
+        const int n = gen_count(a, (int64_t)b * T + e);
+        s_gl[b * T + e] = n;
+        ng += n;
+      }
+      nt += (ng + 31) >> 5;
+    }
+    ntl[b] = nt;
+  }
   __syncthreads();
   for (int b = tid; b < rows; b += 64 * kWgWaves) {
     const int nb = ntl[b];
@@ -836,7 +875,15 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
   const int u1 = __builtin_amdgcn_readfirstlane(order[(U - 1 - i) / H] * H + (U - 1 - i) % H);
   const int b0 = u0 / H, h0 = u0 - b0 * H, b1 = u1 / H, h1 = u1 - b1 * H;
   const SplitRange r0 = split_range(a, b0, 0), r1 = split_range(a, b1, 0);
-  const int nt0 = (int)((r0.total + 31) >> 5), nt1 = (int)((r1.total + 31) >> 5);
+  const int nc0 = (int)((r0.total + 31) >> 5), nc1 = (int)((r1.total + 31) >> 5);  // context tiles
+  // GEN: the units' generated keys (wave-uniform) and, for this lane's query c, its run [glo, ghi) of them
+  auto gen_total = [&](int bu) {
+    int n = 0;
+    for (int e = 0; e < T; ++e) n += s_gl[bu * T + e];
+    return __builtin_amdgcn_readfirstlane(n);
+  };
+  const int ng0 = GEN ? gen_total(b0) : 0, ng1 = GEN ? gen_total(b1) : 0;
+  const int nt0 = nc0 + ((ng0 + 31) >> 5), nt1 = nc1 + ((ng1 + 31) >> 5);
   const int e0 = (nt0 + 1) >> 1, s1 = (nt1 + 1) >> 1;  // half 0: tiles [0, e0) of u0; half 1: [s1, nt1) of u1
   // Wave w takes half 0's tiles w, w + 8, ...  Half 1's tiles go to waves 0..6 only (the last wave publishes half
   // 0 at the switch), round-robin from wave e0 mod 8 on (the waves without an extra half-0 tile first): wave w < 7
@@ -864,6 +911,46 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
     const uint16_t* qrow = qg + (int64_t)((b0 * T + c) * H + h0) * D + g * 8;
 #pragma unroll
     for (int s = 0; s < KS; ++s) qop[s] = c < T ? *reinterpret_cast<const u32x4_t*>(qrow + s * 32) : zero;
+  }
+  int glo = 0, ghi = 0;
+  auto gen_bounds = [&](int bu) {  // query c >= T: an empty run
+    int lo = 0, n = 0;
+    for (int e = 0; e < T; ++e) {
+      const int ne = s_gl[bu * T + e];
+      lo += e < c ? ne : 0;
+      n = e == c ? ne : n;
+    }
+    glo = lo;
+    ghi = lo + n;
+  };
+  const char* kgb0 = nullptr;
+  const char* vgb0 = nullptr;
+  const char* kgb1 = nullptr;
+  const char* vgb1 = nullptr;
+  if constexpr (GEN) {
+    gen_bounds(b0);
+    kgb0 = a.kg + h0 * a.g_head * 2;
+    vgb0 = a.vg + h0 * a.g_head * 2;
+    kgb1 = a.kg + h1 * a.g_head * 2;
+    vgb1 = a.vg + h1 * a.g_head * 2;
+    // The two units' tables: the byte offset of generated key f (beam e, position j) from the head's base, padded
+    // to whole tiles with the unit's last key (a key in use, so the padding reads finite values no query sees).
+    for (int sel = 0; sel < 2; ++sel) {
+      const int bu = sel ? b1 : b0, ngu = sel ? ng1 : ng0;
+      for (int f = tid; f < ((ngu + 31) & ~31); f += 64 * kWgWaves) {
+        const int ff = f < ngu ? f : ngu - 1;
+        int e = 0, base = 0;
+        for (; e < T - 1; ++e) {
+          const int ne = s_gl[bu * T + e];
+          if (ff < base + ne) break;
+          base += ne;
+        }
+        const int j = ff - base;
+        const int64_t src = clamp64(a.ptr[(int64_t)(bu * T + e) * a.ptr_stride + j], 0, a.gen_rows - 1);
+        tab[sel * a.gen_table + f] = (uint32_t)((src * a.g_row + (int64_t)j * D) * 2);
+      }
+    }
+    __syncthreads();
   }
 
   const char* kb0 = reinterpret_cast<const char*>(reinterpret_cast<const uint16_t*>(a.k) + b0 * a.s_row + h0 * a.s_head);
@@ -896,7 +983,16 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
   auto tile_of = [&](int k) { return k < n0 ? w + kWgWaves * k : s1 + j1 + kHalf1Waves * (k - n0); };
   auto ld = [&](KVTile<D>& t, int k) {
     const bool first = k < n0;
-    ld_tile(t, first ? kb0 : kb1, first ? vb0 : vb1, tile_of(k), first ? r0.total : r1.total);
+    const int tile = tile_of(k);
+    if constexpr (GEN) {
+      const int nc = first ? nc0 : nc1;
+      if (tile >= nc) {  // a tile of generated keys (wave-uniform)
+        load_tile_rows<D>(t, first ? kgb0 : kgb1, first ? vgb0 : vgb1,
+                          tab + (first ? 0 : a.gen_table) + (tile - nc) * 32, c, g);
+        return;
+      }
+    }
+    ld_tile(t, first ? kb0 : kb1, first ? vb0 : vb1, tile, first ? r0.total : r1.total);
   };
   auto flush = [&]() {
     float l_tot = st.l_run + __shfl_xor(st.l_run, 16, kWave);
@@ -959,9 +1055,17 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
     for (int s = 0; s < KS; ++s)
       qop[s] = c < T ? *reinterpret_cast<const u32x4_t*>(qs1 + c * D + s * 32 + g * 8) : zero;
     lim = key_limit(r1);
+    if constexpr (GEN) gen_bounds(b1);
   };
   auto at = [&](const KVTile<D>& t, int k) {
-    attend<D>(t, qop, c_scale, st, o, g, tile_of(k) * 32 + 8 * g, lim);
+    const int tile = tile_of(k);
+    if constexpr (GEN) {
+      const int nc = k < n0 ? nc0 : nc1;
+      const bool gt = tile >= nc;  // generated keys: query c's own run of the list
+      attend_range<D>(t, qop, c_scale, st, o, g, (gt ? tile - nc : tile) * 32 + 8 * g, gt ? glo : 0, gt ? ghi : lim);
+    } else {
+      attend<D>(t, qop, c_scale, st, o, g, tile * 32 + 8 * g, lim);
+    }
     if (k == n0 - 1) to_half1();
   };
   if (n0 == 0) to_half1();
@@ -1995,6 +2099,29 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
     a.splits = splits;  // >= 3 slots per unit (see omni_beam_attention_workspace)
     a.counters = counters;
     gen_slot = 2;
+    // Or the generated keys as tiles of the same launch: key rows of D elements, byte offsets from a head's base
+    // within 32 bits, and both units' offset tables within the workgroup's LDS.
+    const int64_t table = ((int64_t)beams * gen_cap + 31) / 32 * 32;
+    const bool fold = gen_pos == head_dim && table <= kPairMaxGenTable &&
+                      ((gen_rows - 1) * gen_row + gen_cap * gen_pos) * 2 <= (int64_t)UINT32_MAX &&
+                      pair_lds_bytes(beams, head_dim, groups, (int)table) <= kPairMaxLds;
+    if (fold) {
+      a.gen_split = -1;
+      a.kg = (const char*)k_gen;
+      a.vg = (const char*)v_gen;
+      a.g_row = gen_row;
+      a.g_head = gen_head;
+      a.ptr = ptr;
+      a.ptr_stride = ptr_stride;
+      a.gen_len = gen_len;
+      a.gen_cap = (int)gen_cap;
+      a.gen_rows = (int)gen_rows;
+      a.gen_table = (int)table;
+      verify_attn_pair_kernel<128, true><<<groups * heads, 64 * kWgWaves,
+                                           pair_lds_bytes(beams, head_dim, groups, (int)table), s>>>(a, groups,
+                                                                                                     a.splits);
+      return omni_launch_status();
+    }
   } else if (balanced) {  // the same order: the generated keys first, then the balanced context launch merging it
     a.counters = counters;
     a.gen_split = 0;  // present; its slot is given by the kernel's balanced layout

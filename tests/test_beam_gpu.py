@@ -98,6 +98,44 @@ def test_beam_attention_context_halves(cuda, beams):
     _beam_case(cuda, torch.bfloat16, 8, beams, 32, 128, keys, 96, ctx_len, gen_len, keys, 71, BF16_TOL)
 
 
+def test_beam_attention_generated_tiles_edges(cuda):
+    """The halves kernel with the generated keys as tiles of its deal, at an odd unit count (43 inputs x 3 heads: the
+    middle workgroup takes both halves of one unit): empty contexts whose generated keys are then all of the unit's
+    tiles (both halves), beams with no generated keys beside beams with many, generated lists longer than the
+    context, finished inputs; the tickets are left zero and a second call gives the same bits."""
+    g = torch.Generator().manual_seed(123)
+    groups, beams = 43, 3
+    ctx_len = torch.randint(0, 400, (groups,), generator=g)
+    ctx_len[::6] = 0
+    gen_len = torch.randint(0, 201, (groups * beams,), generator=g)
+    gen_len[1::4] = 0
+    gen_len[6:9] = 0  # input 2: nothing generated
+    ctx_len[2] = 0  # and no context: a finished input
+    keys = 512
+    a = _beam_case(cuda, torch.bfloat16, groups, beams, 3, 128, keys, 200, ctx_len, gen_len, keys, 124, BF16_TOL)
+    assert torch.all(a[6:9] == 0)
+    torch.cuda.synchronize()
+    assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
+    b = _beam_case(cuda, torch.bfloat16, groups, beams, 3, 128, keys, 200, ctx_len, gen_len, keys, 124, BF16_TOL)
+    assert torch.equal(a, b)
+
+
+def test_beam_attention_halves_long_generation(cuda):
+    """8 inputs x 5 beams x 16 heads x 128 with a generated cache of 1024 positions: more generated positions per
+    unit than the halves kernel's tables hold, so the generated keys run in their own launch and the context halves
+    merge its partial; lengths up to the capacity."""
+    g = torch.Generator().manual_seed(125)
+    ctx_len = torch.tensor([1500, 0, 333, 2000, 1, 900, 64, 1200])
+    gen_len = torch.randint(0, 1025, (40,), generator=g)
+    gen_len[:5] = torch.tensor([1024, 1023, 0, 1, 512])
+    gen_len[5:10] = 0  # input 1 finished
+    keys = 2048
+    out = _beam_case(cuda, torch.bfloat16, 8, 5, 16, 128, keys, 1024, ctx_len, gen_len, keys, 126, BF16_TOL)
+    assert torch.all(out[5:10] == 0)
+    torch.cuda.synchronize()
+    assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
+
+
 @pytest.mark.parametrize("beams", [1, 5, 16])
 def test_beam_attention_wide_balanced(cuda, beams):
     """8 inputs x 8 heads x 512 (the real checkpoint's shape): the context by the balanced wide-head kernel, whose
