@@ -459,17 +459,39 @@ __global__ __launch_bounds__(64, 2) void verify_attn_mfma_kernel(AttnArgs a) {
 // splits (tiles dealt round-robin over them, as in split-K); the partials of a head's workgroups take the head's
 // a.splits slots in workgroup order, so a unit's splits have consecutive slots from ``first``.  Every workgroup
 // computes the same deal from the rows' lengths (rows <= kBalancedMaxRows).  b < 0: no work (every row empty).
+// GEN: a row's tiles are its context tiles and then its beams' generated keys (see verify_attn_slice_kernel), whose
+// counts the deal leaves in gl[row][beam].
 constexpr int kBalancedMaxRows = 64;
+constexpr int kWideMaxBeams = 16;
+constexpr int kWideMaxGenTable = 4096;  // generated keys of a unit taken as tiles of the balanced wide-head kernel
+
+// The generated keys of row ``row`` (a beam) in use.
+__device__ __forceinline__ int gen_count(const AttnArgs& a, int64_t row) {
+  return (int)clamp64(a.gen_len[row], 0, a.gen_cap);
+}
 
 struct BalancedSplit {
   int b, k, nact, first;
 };
 
-__device__ BalancedSplit balanced_split(const AttnArgs& a, int j) {
+template <bool GEN = false>
+__device__ BalancedSplit balanced_split(const AttnArgs& a, int j, int* gl = nullptr) {
   __shared__ int nt[kBalancedMaxRows], wk[kBalancedMaxRows], rem[kBalancedMaxRows];
   __shared__ int s_total, s_given;
   const int tid = threadIdx.x, rows = a.rows, budget = a.splits;  // the launcher ensures rows <= blockDim.x
-  if (tid < rows) nt[tid] = (int)((split_range(a, tid, 0).total + 31) >> 5);
+  if (tid < rows) {
+    int n = (int)((split_range(a, tid, 0).total + 31) >> 5);
+    if constexpr (GEN) {
+      int ng = 0;
+      for (int e = 0; e < a.T; ++e) {
+        const int ne = gen_count(a, (int64_t)tid * a.T + e);
+        gl[tid * a.T + e] = ne;
+        ng += ne;
+      }
+      n += (ng + 31) >> 5;
+    }
+    nt[tid] = n;
+  }
   __syncthreads();
   if (tid == 0) {
     int total = 0;
@@ -518,17 +540,25 @@ __device__ BalancedSplit balanced_split(const AttnArgs& a, int j) {
 // and after one barrier every wave adds the D/128 partials in slice order, so all waves hold the same scores and
 // the same softmax state; each then accumulates its own slice of P V.  Tiles are dealt to the splits as in
 // attend_split; the partials and the last split's merge are those of verify_attn_mfma_kernel.
-template <int D, int G>
+//
+// GEN (beams, balanced): a row's tiles are its context tiles followed by its beams' generated keys -- beam 0's, then
+// beam 1's, ... as one list cut into 32-key tiles, key f at the byte offset the workgroup's table in LDS gives (row
+// ptr[r, j] of the generated cache, position j) -- and query (beam) i sees only its own run [P_i, P_i+1) of that
+// list, so the deal, the pipeline and the merge treat the generated keys like any other tile.
+template <int D, int G, bool GEN = false>
 __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_slice_kernel(AttnArgs a) {
   constexpr int NSL = D / 128;
   __shared__ float sx[2][NSL][G][kWave * 8];  // partial scores of a tile by slice and query group, double-buffered
   __shared__ int s_ticket;
+  // GEN: the rows' generated-key counts [rows][T] and the unit's table of key offsets
+  __shared__ int s_gl[GEN ? kBalancedMaxRows * kWideMaxBeams : 1];
+  __shared__ __align__(16) uint32_t s_tab[GEN ? kWideMaxGenTable : 4];
   const int h = blockIdx.y;
   int sp, b;
   SplitRange r;
   int64_t slot0;  // partial slot of the unit's first split
   if (a.balanced) {
-    const BalancedSplit bs = balanced_split(a, blockIdx.x);
+    const BalancedSplit bs = balanced_split<GEN>(a, blockIdx.x, s_gl);
     if (bs.b < 0) return;  // uniform over the workgroup
     b = bs.b;
     sp = bs.k;
@@ -567,7 +597,47 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
   }
 
   // The split's tiles are k = 0 .. ntot - 1: tile first + k nact of the row.
-  const int64_t row_tiles = (r.total + 31) >> 5;
+  const int ctx_tiles = (int)((r.total + 31) >> 5);
+  int64_t row_tiles = ctx_tiles;
+  // GEN: query 16u + c's run [glo[u], ghi[u]) of the row's generated keys; the table of their offsets
+  int glo[G], ghi[G];
+  const char* kgb = nullptr;
+  const char* vgb = nullptr;
+  if constexpr (GEN) {
+    int ng = 0;
+    for (int e = 0; e < T; ++e) ng += s_gl[b * T + e];
+    ng = __builtin_amdgcn_readfirstlane(ng);
+    row_tiles += (ng + 31) >> 5;
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const int qi = 16 * u + c;
+      int lo = 0, n = 0;
+      for (int e = 0; e < T; ++e) {
+        const int ne = s_gl[b * T + e];
+        lo += e < qi ? ne : 0;
+        n = e == qi ? ne : n;
+      }
+      glo[u] = lo;
+      ghi[u] = lo + n;  // query qi >= T: an empty run
+    }
+    kgb = a.kg + h * a.g_head * 2 + sl * 256;
+    vgb = a.vg + h * a.g_head * 2 + sl * 256;
+    // Key f (beam e, position j) at its byte offset from the head's base, padded to whole tiles with the row's last
+    // key (a key in use: the padding reads finite values no query sees).
+    for (int f = threadIdx.x; f < ((ng + 31) & ~31); f += 64 * NSL) {
+      const int ff = f < ng ? f : ng - 1;
+      int e = 0, base = 0;
+      for (; e < T - 1; ++e) {
+        const int ne = s_gl[b * T + e];
+        if (ff < base + ne) break;
+        base += ne;
+      }
+      const int j = ff - base;
+      const int64_t src = clamp64(a.ptr[(int64_t)(b * T + e) * a.ptr_stride + j], 0, a.gen_rows - 1);
+      s_tab[f] = (uint32_t)((src * a.g_row + (int64_t)j * D) * 2);
+    }
+    __syncthreads();
+  }
   const int64_t first = sp;
   const int64_t ntot = first < row_tiles ? (row_tiles - first + r.nact - 1) / r.nact : 0;
   // The launcher sends only caches with contiguous key rows (s_pos == D) here.
@@ -576,6 +646,13 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
   const int64_t tile_bytes = (int64_t)r.nact * 32 * D * 2;
   const int64_t last_key = a.cache_len - 1;
   auto load_k = [&](KVTile<128>& t, int64_t k) {
+    if constexpr (GEN) {
+      const int ti = (int)(first + k * r.nact);
+      if (ti >= ctx_tiles) {  // a tile of generated keys (wave-uniform)
+        load_tile_rows<128>(t, kgb, vgb, s_tab + (ti - ctx_tiles) * 32, c, g);
+        return;
+      }
+    }
     const int64_t kb = (first + k * r.nact) * 32;
     const int64_t kmax = last_key - kb, vstop = r.total - kb;
     load_tile_clamped<128, D * 2>(t, kt + k * tile_bytes, vt + k * tile_bytes, kmax < 31 ? (int)kmax : 31,
@@ -604,7 +681,12 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
           tot[j + 4] = ww == 0 ? hi[j] : tot[j + 4] + hi[j];
         }
       }
-      attend_scored<128>(t, tot, a.scale_log2, st[u], o[u], g, (int)((first + k * r.nact) * 32) + 8 * g, lim_c[u]);
+      const int ti = (int)(first + k * r.nact);
+      if (GEN && ti >= ctx_tiles)  // generated keys: query 16u + c's own run of the list
+        attend_scored<128, true>(t, tot, a.scale_log2, st[u], o[u], g, (ti - ctx_tiles) * 32 + 8 * g - glo[u],
+                                 ghi[u] - glo[u]);
+      else
+        attend_scored<128>(t, tot, a.scale_log2, st[u], o[u], g, ti * 32 + 8 * g, lim_c[u]);
     }
   };
   // The buffer written for tile k was last read for tile k - 2, before every wave passed tile k - 1's barrier.
@@ -808,11 +890,6 @@ constexpr int kTicketFirst = 1, kTicketClaim = 2, kTicketSecond = 4;
 __host__ __device__ constexpr size_t pair_lds_bytes(int T, int D, int rows = 0, int gen_table = 0) {
   return (size_t)(kWgWaves + 2) * T * (D + 2) * sizeof(float) + (size_t)T * D * 2 +
          (((size_t)rows * T + 3) / 4 * 4 + 2 * (size_t)gen_table) * sizeof(int32_t);
-}
-
-// The generated keys of row ``row`` (a beam) in use.
-__device__ __forceinline__ int gen_count(const AttnArgs& a, int64_t row) {
-  return (int)clamp64(a.gen_len[row], 0, a.gen_cap);
 }
 
 // One 8-wave workgroup per (head, row) unit, working on halves: units are ranked by length, and workgroup i takes
@@ -1442,7 +1519,10 @@ static void launch_balanced_wide(AttnArgs& a, int32_t rows, int32_t heads, int32
   a.chunk = (keys + 31) / 32 * 32;
   a.separate = 0;
   dim3 grid(a.splits, heads, 1);
-  if (head_dim == 256) {
+  if (a.kg) {  // beams with their generated keys as tiles (T <= kWideMaxBeams <= 16: one query group)
+    if (head_dim == 256) verify_attn_slice_kernel<256, 1, true><<<grid, 128, 0, s>>>(a);
+    else verify_attn_slice_kernel<512, 1, true><<<grid, 256, 0, s>>>(a);
+  } else if (head_dim == 256) {
     if (a.T > 16) verify_attn_slice_kernel<256, 2><<<grid, 128, 0, s>>>(a);
     else verify_attn_slice_kernel<256, 1><<<grid, 128, 0, s>>>(a);
   } else {
@@ -2092,6 +2172,23 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
   const bool balanced = !halves && dtype == OMNI_BF16 && ctx_pos == head_dim && counters != nullptr &&
                         balanced_shape(groups, heads, head_dim);
   int gen_splits = splits, gen_slot = ctx_splits;  // where the generated keys' kernel writes: unit slot gen_slot
+  // The generated keys as tiles of the context launch (halves or balanced wide heads): key rows of D elements, byte
+  // offsets from a head's base within 32 bits, a unit's table of offsets (table entries) within the kernel's LDS.
+  const int64_t table = ((int64_t)beams * gen_cap + 31) / 32 * 32;
+  const bool gen_tiles = gen_pos == head_dim && ((gen_rows - 1) * gen_row + gen_cap * gen_pos) * 2 <= (int64_t)UINT32_MAX;
+  auto take_gen = [&]() {
+    a.gen_split = -1;
+    a.kg = (const char*)k_gen;
+    a.vg = (const char*)v_gen;
+    a.g_row = gen_row;
+    a.g_head = gen_head;
+    a.ptr = ptr;
+    a.ptr_stride = ptr_stride;
+    a.gen_len = gen_len;
+    a.gen_cap = (int)gen_cap;
+    a.gen_rows = (int)gen_rows;
+    a.gen_table = (int)table;
+  };
   if (halves) {  // the generated keys' partial first, then the context halves, whose last merge includes it
     a.chunk = (ctx_keys + 31) / 32 * 32;
     a.ctx_splits = 1;
@@ -2099,24 +2196,8 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
     a.splits = splits;  // >= 3 slots per unit (see omni_beam_attention_workspace)
     a.counters = counters;
     gen_slot = 2;
-    // Or the generated keys as tiles of the same launch: key rows of D elements, byte offsets from a head's base
-    // within 32 bits, and both units' offset tables within the workgroup's LDS.
-    const int64_t table = ((int64_t)beams * gen_cap + 31) / 32 * 32;
-    const bool fold = gen_pos == head_dim && table <= kPairMaxGenTable &&
-                      ((gen_rows - 1) * gen_row + gen_cap * gen_pos) * 2 <= (int64_t)UINT32_MAX &&
-                      pair_lds_bytes(beams, head_dim, groups, (int)table) <= kPairMaxLds;
-    if (fold) {
-      a.gen_split = -1;
-      a.kg = (const char*)k_gen;
-      a.vg = (const char*)v_gen;
-      a.g_row = gen_row;
-      a.g_head = gen_head;
-      a.ptr = ptr;
-      a.ptr_stride = ptr_stride;
-      a.gen_len = gen_len;
-      a.gen_cap = (int)gen_cap;
-      a.gen_rows = (int)gen_rows;
-      a.gen_table = (int)table;
+    if (gen_tiles && table <= kPairMaxGenTable && pair_lds_bytes(beams, head_dim, groups, (int)table) <= kPairMaxLds) {
+      take_gen();
       verify_attn_pair_kernel<128, true><<<groups * heads, 64 * kWgWaves,
                                            pair_lds_bytes(beams, head_dim, groups, (int)table), s>>>(a, groups,
                                                                                                      a.splits);
@@ -2124,6 +2205,11 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
     }
   } else if (balanced) {  // the same order: the generated keys first, then the balanced context launch merging it
     a.counters = counters;
+    if (gen_tiles && table <= kWideMaxGenTable && beams <= kWideMaxBeams) {
+      take_gen();
+      launch_balanced_wide(a, groups, heads, head_dim, ctx_keys, s);
+      return omni_launch_status();
+    }
     a.gen_split = 0;  // present; its slot is given by the kernel's balanced layout
     gen_splits = 1;
     gen_slot = heads * balanced_budget(groups, heads);  // slot heads x budget + (group x heads + head)

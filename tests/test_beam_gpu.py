@@ -87,9 +87,9 @@ def test_beam_attention_config5(cuda):
 
 @pytest.mark.parametrize("beams", [3, 5, 11, 12])
 def test_beam_attention_context_halves(cuda, beams):
-    """8 inputs x 32 heads x 128: the context by balanced halves merged with the generated keys' partial (beams <= 11;
-    12 takes split-K) -- finished inputs (no context, no generated keys), a context shorter than a tile, generated keys
-    only."""
+    """8 inputs x 32 heads x 128: the halves kernel with each unit's generated keys as tiles after its context (beams
+    <= 11; 12 takes split-K and the generated keys' own launch) -- finished inputs (no context, no generated keys), a
+    context shorter than a tile, generated keys only."""
     g = torch.Generator().manual_seed(70 + beams)
     ctx_len = torch.tensor([2300, 0, 17, 1500, 0, 640, 999, 33])
     gen_len = torch.randint(0, 97, (8 * beams,), generator=g)
@@ -120,17 +120,19 @@ def test_beam_attention_generated_tiles_edges(cuda):
     assert torch.equal(a, b)
 
 
-def test_beam_attention_halves_long_generation(cuda):
-    """8 inputs x 5 beams x 16 heads x 128 with a generated cache of 1024 positions: more generated positions per
-    unit than the halves kernel's tables hold, so the generated keys run in their own launch and the context halves
-    merge its partial; lengths up to the capacity."""
+@pytest.mark.parametrize("h,d", [(16, 128), (8, 512)])
+def test_beam_attention_long_generation(cuda, h, d):
+    """8 inputs x 5 beams with a generated cache of 1024 positions: more generated positions per unit than the
+    context kernels' tables hold (the halves kernel at 16 heads x 128, the balanced wide-head kernel at 8 x 512), so
+    the generated keys run in their own launch and the context launch merges its partial; lengths up to the
+    capacity."""
     g = torch.Generator().manual_seed(125)
     ctx_len = torch.tensor([1500, 0, 333, 2000, 1, 900, 64, 1200])
     gen_len = torch.randint(0, 1025, (40,), generator=g)
     gen_len[:5] = torch.tensor([1024, 1023, 0, 1, 512])
     gen_len[5:10] = 0  # input 1 finished
     keys = 2048
-    out = _beam_case(cuda, torch.bfloat16, 8, 5, 16, 128, keys, 1024, ctx_len, gen_len, keys, 126, BF16_TOL)
+    out = _beam_case(cuda, torch.bfloat16, 8, 5, h, d, keys, 1024, ctx_len, gen_len, keys, 126, BF16_TOL)
     assert torch.all(out[5:10] == 0)
     torch.cuda.synchronize()
     assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
@@ -138,9 +140,10 @@ def test_beam_attention_halves_long_generation(cuda):
 
 @pytest.mark.parametrize("beams", [1, 5, 16])
 def test_beam_attention_wide_balanced(cuda, beams):
-    """8 inputs x 8 heads x 512 (the real checkpoint's shape): the context by the balanced wide-head kernel, whose
-    last workgroup of each (input, head) merges the context splits with the generated keys' partial -- finished
-    inputs (no context, no generated keys), a context shorter than a tile, generated keys only, up to 16 beams."""
+    """8 inputs x 8 heads x 512 (the real checkpoint's shape): the balanced wide-head kernel with each input's
+    generated keys as tiles after its context, dealt with them over the (input, head)'s workgroups, whose last one
+    merges the splits -- finished inputs (no context, no generated keys), a context shorter than a tile, generated
+    keys only, up to 16 beams."""
     g = torch.Generator().manual_seed(90 + beams)
     ctx_len = torch.tensor([2300, 0, 17, 1500, 0, 640, 999, 33])
     gen_len = torch.randint(0, 97, (8 * beams,), generator=g)
