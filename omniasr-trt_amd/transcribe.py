@@ -1,27 +1,31 @@
-"""The decoder side of omniASR-LLM's streaming transcription: segment contexts, the choice of decoder, and CTC-frame
+"""The decoder side of omniASR-LLM's streaming transcription: segment prompts, the choice of decoder, and CTC-frame
 drafts fed to the drafted decoder.
 
 What the reference's ``LLMTranscriber`` does between its audio encoder and its tokenizer
-(src/omniasr_trt/llm.py:88-340), on audio that is already embedded: an input is cut into 15 s segments, and segment
-i is decoded with segment i-1's audio and text as its context,
+(src/omniasr_trt/llm.py:88-340), on audio that is already embedded.  An input is cut into 15 s segments, and
+segment i is decoded with segment i-1's audio and text in its prompt,
 
     [lang] <lid> (audio_{i-1} <regular> <bos> text_{i-1} <eos>) audio_i <last|regular> <bos> -> text_i <eos>
 
-(src/omniasr_trt/llm.py:160-173); every input's segments run one after another as one stream of the decoder, and the
-inputs share the decoder's slots.  With ``draft_tokens`` > 0 the greedy search is the drafted decoder, and each
+(src/omniasr_trt/llm.py:160-173).  Every input's segments run one after another as one stream of the decoder, and
+the inputs share the decoder's slots.  With ``draft_tokens`` > 0 the greedy search is the drafted decoder, and each
 segment's draft is the CTC transcript of its frames and a margin around them (:meth:`llm.Row.draft`), handed to the
-decoder through its ``drafts`` callback when the segment's context is admitted (src/omniasr_trt/llm.py:315-340).
+decoder through its ``drafts`` callback when the segment is admitted (src/omniasr_trt/llm.py:315-340).
 
 The encoder (wav2vec2 + projection), the CTC model and the tokenizer are not part of the decode step and are not
 here: an input is given as its segments' decoder embeddings ``[F_i, model_dim]``, a drafter as an object with
 ``frame_ids(audio) -> per input CTC argmax of each 20 ms frame``, and the result is token ids (or text, with a
 tokenizer that has ``decode(ids)``).
+
+Three parts: :class:`PromptLayout` states the prompt above as data, :class:`DecoderPool` keeps one decoder per search
+setting (only the one in use holds caches), and :class:`SegmentStreams` feeds a decoder's stream callbacks from the
+inputs' segments.  :class:`Transcriber` puts them together.
 """
 
 from __future__ import annotations
 
 import time
-from contextlib import contextmanager
+from contextlib import contextmanager, nullcontext
 
 import numpy as np
 import torch
@@ -34,135 +38,186 @@ from .modeling import DecoderModel
 from .spec import SpecDecoder
 
 
+class PromptLayout:
+    """The decoder prompt of segment i of an input (src/omniasr_trt/llm.py:160-173), built from a list of parts: an
+    embedding row range, a run of text token ids, or audio embeddings.  The special ids follow the text vocabulary:
+    <lid>, <last segment>, <regular segment>."""
+
+    def __init__(self, model: DecoderModel, dtype: torch.dtype, device: torch.device):
+        self.model, self.dtype, self.device = model, dtype, device
+        vocab = model.dec_cfg.vocab_size
+        self.lid, self.last_seg, self.regular_seg = vocab, vocab + 1, vocab + 2
+
+    def parts(self, row: Row, i: int) -> list[tuple[str, object]]:
+        """(kind, value) parts in prompt order: "lang" (a language embedding row), "ids" (text ids), "audio"."""
+        closing = self.last_seg if i == row.segments - 1 else self.regular_seg
+        history = [("audio", row.audio[i - 1]), ("ids", [self.regular_seg, BOS, *row.tokens[i - 1], EOS])] if i else []
+        return [("lang", row.lang), ("ids", [self.lid]), *history, ("audio", row.audio[i]), ("ids", [closing, BOS])]
+
+    def embed(self, parts: list[tuple[str, object]]) -> Tensor:
+        """The parts' embeddings ``[C, D]`` in the model's dtype."""
+        rows = []
+        for kind, value in parts:
+            if kind == "lang":
+                rows.append(self.model.lang_embeddings.weight[value: value + 1])
+            elif kind == "ids":
+                rows.append(self.model.text_frontend.weight[torch.tensor(value, dtype=torch.long, device=self.device)])
+            else:
+                rows.append(value)
+        return torch.cat([r.to(self.dtype) for r in rows])
+
+    def __call__(self, row: Row, i: int) -> Tensor:
+        return self.embed(self.parts(row, i))
+
+
+def search_key(beams: int, length_norm: bool, draft_tokens: int) -> tuple:
+    """The decoder a search runs on (src/omniasr_trt/llm.py:284-313): beam search unless it is one beam without length
+    normalisation; then the drafted greedy decoder with ``draft_tokens`` > 0, the one-token greedy decoder with 0."""
+    if beams != 1 or length_norm:
+        return ("beam", beams, length_norm)
+    return ("spec", draft_tokens) if draft_tokens > 0 else ("greedy",)
+
+
+class DecoderPool:
+    """One decoder per search key, built on first use; taking one releases the caches of every other, so only the
+    decoder in use holds device memory."""
+
+    def __init__(self, model: DecoderModel, max_batch: int, reserve: int):
+        self.model, self.max_batch, self.reserve = model, max_batch, reserve
+        self.decoders: dict[tuple, object] = {}
+
+    def _build(self, key: tuple):
+        kind = key[0]
+        if kind == "spec":
+            return SpecDecoder(self.model, draft_tokens=key[1], max_batch=self.max_batch, reserve=self.reserve)
+        if kind == "greedy":
+            return GreedyDecoder(self.model, max_batch=self.max_batch, reserve=self.reserve)
+        return BeamDecoder(self.model, beams=key[1], length_norm=key[2], max_batch=self.max_batch,
+                           reserve=self.reserve)
+
+    def take(self, key: tuple):
+        dec = self.decoders.get(key)
+        if dec is None:
+            dec = self.decoders[key] = self._build(key)
+        for other_key, other in self.decoders.items():
+            holds = getattr(other, "capacity", 0) or getattr(other, "ccap", 0)
+            if other_key != key and holds:
+                other.release()
+        return dec
+
+
+class SegmentStreams:
+    """The stream callbacks of ``decode_streams`` over the inputs' rows: stream j opens with segment 0's prompt, and
+    each finished segment's tokens go into the row and yield the next segment's prompt (None after the last)."""
+
+    def __init__(self, rows: list[Row], prompt, timed):
+        self.rows, self.prompt, self.timed = rows, prompt, timed
+
+    def first(self, j: int) -> Tensor:
+        with self.timed("context"):
+            return self.prompt(self.rows[j], 0)
+
+    def advance(self, j: int, tokens: list[int]) -> Tensor | None:
+        row = self.rows[j]
+        row.tokens.append(tokens)
+        if len(row.tokens) == row.segments:
+            return None
+        with self.timed("context"):
+            return self.prompt(row, len(row.tokens))
+
+    def draft(self, j: int):
+        """The CTC draft of stream j's segment now being admitted (the segment after its finished ones)."""
+        row = self.rows[j]
+        return row.draft(len(row.tokens))
+
+
 class Transcriber:
-    """Streaming transcription of embedded audio with the MI355X decoders; the reference's ``LLMTranscriber``
+    """Streaming transcription of embedded audio with the MI355X decoders, taking the reference's ``LLMTranscriber``
     constructor options that concern decoding (src/omniasr_trt/llm.py:88-109)."""
 
     def __init__(self, model: DecoderModel, tokenizer=None, *, max_batch: int = 8, reserve: int = 512, beams: int = 1,
                  length_norm: bool = False, drafter=None, draft_tokens: int = 4):
         self.model = model
         self.tokenizer = tokenizer
-        self.max_batch = max_batch
-        self.reserve = reserve
         self.beams, self.length_norm = beams, length_norm  # search defaults (beams 1: greedy)
         self.drafter = drafter  # None: the drafted search proposes from each row's own tokens only
         self.draft_tokens = draft_tokens  # tokens proposed per drafted step (0: one token per step)
-        vocab = model.dec_cfg.vocab_size
-        self.lid, self.last_seg, self.regular_seg = vocab, vocab + 1, vocab + 2  # special text embedding rows
-        self.dtype = model.final_proj.weight.dtype
-        self.device = model.final_proj.weight.device
-        self._decoders: dict = {}
+        weight = model.final_proj.weight
+        self.layout = PromptLayout(model, weight.dtype, weight.device)
+        self.pool = DecoderPool(model, max_batch, reserve)
         self.last_decoder = None
-        self.profile = False  # True: each phase synchronises the device and adds its seconds to ``timings``
+        self.profile = False  # True: each named phase synchronises the device and adds its seconds to ``timings``
         self.timings: dict[str, float] = {}
 
+    @property
+    def device(self) -> torch.device:
+        return self.layout.device
+
+    def timed(self, name: str):
+        """A context manager around one named phase: a no-op unless ``profile`` is set."""
+        return self._timed(name) if self.profile else nullcontext()
+
     @contextmanager
-    def phase(self, name: str):
-        if not self.profile:
-            yield
-            return
+    def _timed(self, name: str):
         torch.cuda.synchronize(self.device)
-        t0 = time.perf_counter()
+        start = time.perf_counter()
         try:
             yield
         finally:
             torch.cuda.synchronize(self.device)
-            self.timings[name] = self.timings.get(name, 0.0) + time.perf_counter() - t0
+            self.timings[name] = self.timings.get(name, 0.0) + time.perf_counter() - start
 
-    # ------------------------------------------------------------------ audio segments and prompts
+    # ------------------------------------------------------------------ inputs and outputs
 
     def rows(self, audio: list, langs=None, drafts=None) -> list[Row]:
         """One :class:`Row` per input: ``audio[j]`` the list of its segments' embeddings, ``langs[j]`` its language
         embedding row (None: 0), ``drafts[j]`` its CTC frame argmaxes (None: no draft)."""
-        langs = [None] * len(audio) if langs is None else list(langs)
-        drafts = [None] * len(audio) if drafts is None else list(drafts)
-        if not len(audio) == len(langs) == len(drafts):
+        n = len(audio)
+        langs = [None] * n if langs is None else list(langs)
+        drafts = [None] * n if drafts is None else list(drafts)
+        if len(langs) != n or len(drafts) != n:
             raise ValueError("audio, langs and drafts: one entry per input")
         out = []
-        for j, (segs, lang, frames) in enumerate(zip(audio, langs, drafts)):
-            segs = [s.to(self.device, self.dtype) for s in segs]
-            if not segs:
+        for j in range(n):
+            if not audio[j]:
                 raise ValueError(f"input {j}: no segment")
-            out.append(Row(index=j, segments=len(segs), lang=0 if lang is None else int(lang), audio=segs,
-                           frames=as_frames(frames)))
+            segments = [s.to(self.device, self.layout.dtype) for s in audio[j]]
+            out.append(Row(index=j, segments=len(segments), lang=int(langs[j] or 0), audio=segments,
+                           frames=as_frames(drafts[j])))
         return out
 
-    def context(self, r: Row, i: int) -> Tensor:
-        """Decoder input embeddings ``[C, D]`` of segment ``i`` of row ``r``, ending with <bos>
-        (src/omniasr_trt/llm.py:160-173)."""
-        text = self.model.text_frontend.weight
+    def context(self, row: Row, i: int) -> Tensor:
+        """Decoder input embeddings ``[C, D]`` of segment ``i`` of ``row``, ending with <bos>."""
+        return self.layout(row, i)
 
-        def ids(values: list[int]) -> Tensor:
-            return text[torch.tensor(values, dtype=torch.long, device=self.device)]
-
-        pieces = [self.model.lang_embeddings.weight[r.lang: r.lang + 1], ids([self.lid])]
-        if i > 0:  # the previous segment, audio and text, as context
-            pieces += [r.audio[i - 1], ids([self.regular_seg, BOS, *r.tokens[i - 1], EOS])]
-        marker = self.last_seg if i == r.segments - 1 else self.regular_seg
-        pieces += [r.audio[i], ids([marker, BOS])]
-        return torch.cat([p.to(self.dtype) for p in pieces])
-
-    def text(self, r: Row):
-        ids = [t for seg in r.tokens for t in seg if t not in (PAD, BOS, EOS)]
+    def result(self, row: Row):
+        ids = [t for segment in row.tokens for t in segment if t not in (PAD, BOS, EOS)]
         return ids if self.tokenizer is None else self.tokenizer.decode(ids)
 
     # ------------------------------------------------------------------ decoding
 
     def decoder(self, beams: int, length_norm: bool):
-        """The decoder for this search, one kept per setting (the others' caches are released): the drafted decoder
-        for greedy search with ``draft_tokens`` > 0, the one-token greedy decoder with 0, beam search otherwise.
-        (src/omniasr_trt/llm.py:284-313)"""
-        greedy = beams == 1 and not length_norm
-        if greedy:
-            key = ("spec", self.draft_tokens) if self.draft_tokens > 0 else ("greedy",)
-        else:
-            key = ("beam", beams, length_norm)
-        dec = self._decoders.get(key)
-        if dec is None:
-            if key[0] == "spec":
-                dec = SpecDecoder(self.model, draft_tokens=self.draft_tokens, max_batch=self.max_batch,
-                                  reserve=self.reserve)
-            elif key[0] == "greedy":
-                dec = GreedyDecoder(self.model, max_batch=self.max_batch, reserve=self.reserve)
-            else:
-                dec = BeamDecoder(self.model, beams=beams, length_norm=length_norm, max_batch=self.max_batch,
-                                  reserve=self.reserve)
-            self._decoders[key] = dec
-        for other_key, other in self._decoders.items():
-            if other_key != key and (getattr(other, "capacity", 0) or getattr(other, "ccap", 0)):
-                other.release()
-        dec.phase = self.phase
+        """The decoder of this search (see :func:`search_key`); the pool releases the others' caches."""
+        dec = self.pool.take(search_key(beams, length_norm, self.draft_tokens))
+        dec.phase = self.timed
         self.last_decoder = dec
         return dec
 
     def transcribe_rows(self, rows: list[Row], beams: int = 1, length_norm: bool = False) -> list:
-        """Decode every segment of every row: each row is one stream of contexts (segment i + 1's context holds
-        segment i's tokens), the rows share the decoder's slots.  The drafted decoder takes each segment's draft from
-        the row's CTC frames when the segment is admitted.  (src/omniasr_trt/llm.py:315-340)"""
+        """Decode every segment of every row as one stream per row; the rows share the decoder's slots, and the
+        drafted decoder takes each segment's draft from the row's CTC frames as the segment is admitted."""
         dec = self.decoder(beams, length_norm)
+        streams = SegmentStreams(rows, self.layout, self.timed)
         drafted = isinstance(dec, SpecDecoder)
         if drafted:
-            dec.drafts = lambda j: rows[j].draft(len(rows[j].tokens))
-
-        def first_context(j: int) -> Tensor:
-            with self.phase("context"):
-                return self.context(rows[j], 0)
-
-        def next_context(j: int, tokens: list[int]) -> Tensor | None:
-            r = rows[j]
-            r.tokens.append(tokens)
-            if len(r.tokens) == r.segments:
-                return None
-            with self.phase("context"):
-                return self.context(r, len(r.tokens))
-
+            dec.drafts = streams.draft
         try:
-            with self.phase("decoder"):
-                dec.decode_streams(len(rows), first_context, next_context)
+            with self.timed("decoder"):
+                dec.decode_streams(len(rows), streams.first, streams.advance)
         finally:
             if drafted:
                 dec.drafts = lambda j: None  # the rows (their embeddings) are not held after the call
-        return [self.text(r) for r in rows]
+        return [self.result(r) for r in rows]
 
     @torch.inference_mode()
     def transcribe(self, audio: list, langs=None, *, mode: str = "fast", beams: int | None = None,
@@ -177,12 +232,13 @@ class Transcriber:
                              "'reference' loops are not part of this package")
         beams = self.beams if beams is None else beams
         length_norm = self.length_norm if length_norm is None else length_norm
-        greedy = beams == 1 and not length_norm
-        if drafts is None and self.drafter is not None and greedy and self.draft_tokens:
-            with self.phase("drafter"):
+        drafted = search_key(beams, length_norm, self.draft_tokens)[0] == "spec"
+        if not drafted:
+            drafts = None  # only the drafted search reads frames
+        elif drafts is None and self.drafter is not None:
+            with self.timed("drafter"):
                 drafts = self.drafter.frame_ids(audio)
-        rows = self.rows(audio, langs, drafts if greedy else None)
-        return self.transcribe_rows(rows, beams, length_norm)
+        return self.transcribe_rows(self.rows(audio, langs, drafts), beams, length_norm)
 
 
 def frames_from_tokens(segments: list[list[int]], frames_per_segment: int, rng: np.random.Generator,
@@ -207,4 +263,4 @@ def frames_from_tokens(segments: list[list[int]], frames_per_segment: int, rng: 
     return out
 
 
-__all__ = ["Transcriber", "frames_from_tokens"]
+__all__ = ["DecoderPool", "PromptLayout", "SegmentStreams", "Transcriber", "frames_from_tokens", "search_key"]

@@ -91,3 +91,35 @@ def test_synthetic_frames_give_back_each_segments_tokens(monkeypatch):
     noisy = frames_from_tokens(segments, 100, np.random.default_rng(4), substitute=0.5, vocab=50)
     ids, before = llm.Row(index=0, segments=5, frames=noisy).draft(2)
     assert ids[before: before + 33] != segments[2] and len(ids[before: before + 33]) == 33
+
+
+def test_prompt_layout_and_search_choice():
+    """The transcriber's segment prompt (src/omniasr_trt/llm.py:160-173): [lang] <lid> (audio_{i-1} <regular> <bos>
+    text_{i-1} <eos>) audio_i <last|regular> <bos>, with the three markers after the text vocabulary; and the decoder
+    each search runs on (llm.py:284-313)."""
+    from omniasr_trt_amd import transcribe
+
+    cfg = modeling.DecoderConfig(model_dim=16, num_layers=1, num_heads=2, ffn_dim=24, vocab_size=12, num_langs=5)
+    m = modeling.DecoderModel(cfg)
+    t = transcribe.Transcriber(m)
+    g = torch.Generator().manual_seed(3)
+    (row,) = t.rows([[torch.randn(4, 16, generator=g), torch.randn(2, 16, generator=g), torch.randn(3, 16, generator=g)]],
+                    langs=[3])
+    row.tokens += [[5, 6], [7]]
+    lid, last, regular = 12, 13, 14
+    assert t.layout.parts(row, 0)[1] == ("ids", [lid]) and t.layout.parts(row, 0)[-1] == ("ids", [regular, llm.BOS])
+    assert t.layout.parts(row, 2)[-1] == ("ids", [last, llm.BOS])  # the input's last segment
+    assert t.layout.parts(row, 1)[3] == ("ids", [regular, llm.BOS, 5, 6, llm.EOS])
+    text, langs = m.text_frontend.weight, m.lang_embeddings.weight
+    for i in range(3):
+        want = [langs[3:4], text[[lid]]]
+        if i:
+            want += [row.audio[i - 1], text[[regular, llm.BOS, *row.tokens[i - 1], llm.EOS]]]
+        want += [row.audio[i], text[[last if i == 2 else regular, llm.BOS]]]
+        assert torch.equal(t.context(row, i), torch.cat(want)), i
+    assert transcribe.search_key(1, False, 4) == ("spec", 4)
+    assert transcribe.search_key(1, False, 0) == ("greedy",)
+    assert transcribe.search_key(5, False, 4) == ("beam", 5, False)
+    assert transcribe.search_key(1, True, 4) == ("beam", 1, True)  # length normalisation is a beam search
+    with pytest.raises(ValueError):
+        t.rows([[torch.zeros(1, 16)]], langs=[0, 1])

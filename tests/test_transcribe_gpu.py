@@ -130,7 +130,7 @@ def test_decoder_choice(case, monkeypatch):
     say("transcriber: beam search with 3 beams (segment by segment, against the decoder run directly)")
     got = t.transcribe(inputs, langs, beams=3)
     assert isinstance(t.last_decoder, BeamDecoder) and t.last_decoder.beams == 3
-    assert t._decoders[("greedy",)].capacity == 0
+    assert t.pool.decoders[("greedy",)].capacity == 0
     # the same search run by hand: each input's segments in order, contexts from the beam tokens
     direct = BeamDecoder(m, beams=3, max_batch=3, reserve=16)
     for j, audio in enumerate(inputs):
