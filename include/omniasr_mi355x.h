@@ -170,13 +170,14 @@ size_t omni_beam_attention_workspace(int32_t groups, int32_t beams, int32_t head
  * (strides gen_row / gen_head / gen_pos, ``gen_rows`` rows of ``gen_cap`` positions); pointers are
  * clamped into [0, gen_rows).  out = softmax(q.k * scale) . v over both parts, fp32 accumulation; no
  * key at all gives zeros.  One pass over a group's context serves all of its beams (the kernels of
- * omni_verify_attention with every query over the same keys); the generated keys are read by a
- * pointer-chasing kernel into one more partial.  bf16, head_dim 128, contiguous key rows, beams <= 11 and
- * groups * heads >= 128: the context halves kernel merges that partial in its last step; bf16, head_dim 256 /
- * 512, contiguous key rows, groups <= 64: the balanced wide-head kernel does (``counters``: groups*heads int32
- * tickets, zero before the first call, left zero); otherwise split-K and a merge launch.
- * ``chunk``: context keys per split (0: the library's choice).  ``workspace``: at least
- * omni_beam_attention_workspace() bytes, 256-byte aligned.  beams: 1..16.
+ * omni_verify_attention with every query over the same keys).  bf16, head_dim 128, contiguous key rows,
+ * beams <= 11 and groups * heads >= 128: the context halves kernel; bf16, head_dim 256 / 512, contiguous key rows,
+ * groups <= 64: the balanced wide-head kernel (``counters``: groups*heads int32 tickets, zero before the first
+ * call, left zero).  In both, when beams * gen_cap <= 4096 and the generated cache's byte offsets fit 32 bits,
+ * each group's generated keys (beam 0's, then beam 1's, ...) are tiles of the same launch after its context;
+ * otherwise they are read by a pointer-chasing launch into one more partial that the context's merge takes.
+ * Other shapes: split-K and a merge launch.  ``chunk``: context keys per split (0: the library's choice).
+ * ``workspace``: at least omni_beam_attention_workspace() bytes, 256-byte aligned.  beams: 1..16.
  */
 int omni_beam_attention(const void *q, const void *k_ctx, const void *v_ctx, int64_t ctx_row,
                         int64_t ctx_head, int64_t ctx_pos, int64_t ctx_cap, const int64_t *ctx_len,
@@ -186,6 +187,40 @@ int omni_beam_attention(const void *q, const void *k_ctx, const void *v_ctx, int
                         int32_t heads, int32_t head_dim, int32_t ctx_keys, int32_t chunk, float scale,
                         void *out, void *workspace, size_t workspace_bytes, int32_t *counters,
                         int32_t dtype, void *stream);
+
+/*
+ * Each group's generated keys listed once per distinct (row, position).  No counterpart in the reference: the
+ * beams of a group share most of their history (ptr rows copied from their parents, src/omniasr_trt/beam.py:
+ * 170-187), so most generated keys are the same cache row and position for several beams; built once per search
+ * step, the list lets omni_beam_attention_listed read each such key once for all the beams that see it.  For beam
+ * decoders that call the attention layer by layer with one set of pointers per step.
+ *
+ * Group g (rows g*beams .. g*beams+beams-1; ``ptr``, ``gen_len``, ``gen_cap``, ``gen_rows`` as for
+ * omni_beam_attention): list[g*list_stride + f] is the byte offset of key f from a generated cache's base, without
+ * its head (row * gen_row + position * gen_pos elements, times 2), mask[g*list_stride + f] the beams that see it
+ * (bit i: beam i), count[g] the list's length.  Order: by position, then by the first beam that reaches the key.
+ * list_stride >= beams * gen_cap; beams: 1..16; the offsets must fit 32 bits (OMNI_ERR_SHAPE otherwise).
+ */
+int omni_beam_gen_list(int32_t groups, int32_t beams, const int32_t *ptr, int64_t ptr_stride, const int64_t *gen_len,
+                       int64_t gen_cap, int64_t gen_rows, int64_t gen_row, int64_t gen_pos, uint32_t *list,
+                       uint16_t *mask, int32_t *count, int64_t list_stride, void *stream);
+
+/*
+ * omni_beam_attention with the lists of omni_beam_gen_list (built from the same ptr / gen_len and the generated
+ * caches' strides, on the same stream before the call): where the generated keys are tiles of the context launch,
+ * they are each group's listed keys, each seen by the beams of its mask; elsewhere the lists are not used.  No
+ * counterpart in the reference (see omni_beam_gen_list); the results equal omni_beam_attention's up to the order of
+ * the floating-point sums.
+ */
+int omni_beam_attention_listed(const void *q, const void *k_ctx, const void *v_ctx, int64_t ctx_row,
+                               int64_t ctx_head, int64_t ctx_pos, int64_t ctx_cap, const int64_t *ctx_len,
+                               const void *k_gen, const void *v_gen, int64_t gen_row, int64_t gen_head,
+                               int64_t gen_pos, int64_t gen_cap, int64_t gen_rows, const int32_t *ptr,
+                               int64_t ptr_stride, const int64_t *gen_len, const uint32_t *gen_list,
+                               const uint16_t *gen_mask, const int32_t *gen_count, int64_t list_stride,
+                               int32_t groups, int32_t beams, int32_t heads, int32_t head_dim, int32_t ctx_keys,
+                               int32_t chunk, float scale, void *out, void *workspace, size_t workspace_bytes,
+                               int32_t *counters, int32_t dtype, void *stream);
 
 /*
  * Causal attention over whole contexts: the prefill's

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: its HIP runtime is the one the library uses)
 
 PATH = Path(__file__).resolve().with_name("libomniasr_mi355x.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK = 0
 F32, BF16 = 0, 1
@@ -42,6 +42,12 @@ _SIGNATURES = {
     "omni_beam_attention": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, c_int64, c_int64,
                                     c_int64, c_int64, c_int64, _P, c_int64, _P, c_int32, c_int32, c_int32, c_int32,
                                     c_int32, c_int32, c_float, _P, _P, c_size_t, _P, c_int32, _P]),
+    "omni_beam_gen_list": (c_int, [c_int32, c_int32, _P, c_int64, _P, c_int64, c_int64, c_int64, c_int64, _P, _P, _P,
+                                   c_int64, _P]),
+    "omni_beam_attention_listed": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, c_int64,
+                                           c_int64, c_int64, c_int64, c_int64, _P, c_int64, _P, _P, _P, _P, c_int64,
+                                           c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_float, _P, _P,
+                                           c_size_t, _P, c_int32, _P]),
     "omni_prefill_attention": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, _P, c_int32, c_int32,
                                        c_int32, c_int32, c_float, _P, c_int32, _P]),
     "omni_propose": (c_int, [_P, c_int64, c_int64, _P, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int32,

@@ -77,6 +77,7 @@ class BeamDecoder(GreedyDecoder):
         self.ctx_len = torch.zeros(max_batch, dtype=torch.long, device=dev)
         self.gen_len = torch.zeros(rows, dtype=torch.long, device=dev)
         self.kc = self.vc = self.kg = self.vg = self.ptr = self.hist = None
+        self.gen_list = None  # bf16: each group's generated keys once per distinct (row, position), built every step
         self.ccap = self.gcap = 0
         self._normal_caps: tuple[int, int] | None = None
         self.stats["repetition_stops"] = 0
@@ -109,13 +110,15 @@ class BeamDecoder(GreedyDecoder):
             self.vg = _regrown(self.vg, shape, 3, 0, dt, dev)
             self.ptr = _regrown(self.ptr, (rows, want_g), 1, 0, torch.int32, dev)
             self.hist = _regrown(self.hist, (rows, want_g + 1), 1, PAD, torch.int32, dev)
+            if dt == torch.bfloat16:
+                self.gen_list = kernels.GenList(self.groups, self.beams, want_g, dev)
             self.stats["grows"] += bool(self.gcap)
             self.gcap = want_g
         self.reset_graphs()
 
     def release(self) -> None:
         torch.cuda.synchronize(self.device)
-        self.kc = self.vc = self.kg = self.vg = self.ptr = self.hist = None
+        self.kc = self.vc = self.kg = self.vg = self.ptr = self.hist = self.gen_list = None
         self.ccap = self.gcap = 0
         self.reset_graphs()
 
@@ -147,6 +150,9 @@ class BeamDecoder(GreedyDecoder):
         kernels.beam_prepare(s, n, self.ctx, self.k_step, self.gdone, ptr, self.row_pos, self.gen_pos, self.ctx_len,
                              self.gen_len)
         pos, gen_pos, ctx_len, gen_len = self.row_pos[:r], self.gen_pos[:r], self.ctx_len[:s], self.gen_len[:r]
+        lst = self.gen_list
+        if lst is not None:  # the beams share most generated keys: list each once for every layer of the step
+            kernels.beam_gen_list(lst, ptr, gen_len, self.kg[0], s)
         scale = self.head_dim ** -0.5
         h = self.m.text_frontend.weight[self.tok[:r]]
         for i in range(len(self.layers)):
@@ -155,7 +161,7 @@ class BeamDecoder(GreedyDecoder):
             def attend(qkv, i=i, kg=kg, vg=vg):
                 q = kernels.rope_kv(qkv, self.m.rope, pos, kg, vg, self.heads, None, gen_pos)
                 return kernels.beam_attention(q, self.kc[i], self.vc[i], ctx_len, kg, vg, ptr, gen_len, n, ckeys,
-                                              scale).reshape(r, -1)
+                                              scale, gen_list=lst).reshape(r, -1)
 
             self._layer(i, h, attend)
         logits = self._head(h)  # [R, V]

@@ -153,14 +153,15 @@ struct SoftmaxState {
 
 // A tile with its raw scores ``sv`` (lane (c, g): query c, keys key0 + j): the causal / end-of-row mask (key0 + j >=
 // lim: query c does not see key j of this lane), the lazy reference max, probabilities, O += P V.  The mask is a no-op
-// on tiles every query sees whole.  kRange: the mask is 0 <= key0 + j < lim (keys numbered from a range's start).
-template <int D, bool kRange = false>
+// on tiles every query sees whole.  kBits: ``lim`` holds this lane's mask instead, bit j set when query c sees key
+// key0 + j (key0 unused).
+template <int D, bool kBits = false>
 __device__ __forceinline__ void attend_scored(const KVTile<D>& t, float (&sv)[8], float c_scale, SoftmaxState& st,
                                               f32x4_t (&o)[D / 16], int g, int key0, int lim) {
   bool over = false;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const bool seen = kRange ? (uint32_t)(key0 + j) < (uint32_t)lim : key0 + j < lim;
+    const bool seen = kBits ? ((lim >> j) & 1) != 0 : key0 + j < lim;
     sv[j] = seen ? sv[j] : -INFINITY;
     over |= sv[j] > st.thr;
   }
@@ -194,16 +195,13 @@ __device__ __forceinline__ void attend(const KVTile<D>& t, const u32x4_t (&qop)[
   attend_scored<D>(t, sv, c_scale, st, o, g, key0, lim);
 }
 
-// One tile whose keys query c sees form the range [lo, lim) of the tile's numbering (key0 + j for this lane's keys):
-// a range that starts at 0 is attend's mask; a range inside a list of several queries' keys selects query c's own.
+// One tile whose keys each query sees by a mask: bit j of ``bits`` says whether query c sees key 8g + j.
 template <int D>
-__device__ __forceinline__ void attend_range(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float c_scale,
-                                             SoftmaxState& st, f32x4_t (&o)[D / 16], int g, int key0, int lo,
-                                             int lim) {
+__device__ __forceinline__ void attend_bits(const KVTile<D>& t, const u32x4_t (&qop)[D / 32], float c_scale,
+                                            SoftmaxState& st, f32x4_t (&o)[D / 16], int g, int bits) {
   float sv[8];
   tile_scores<D>(t, qop, sv);
-  // key0 + j in [lo, lim): the keys renumbered from lo, then one unsigned compare
-  attend_scored<D, true>(t, sv, c_scale, st, o, g, key0 - lo, lim > lo ? lim - lo : 0);
+  attend_scored<D, true>(t, sv, c_scale, st, o, g, 0, bits);
 }
 
 // A workgroup barrier ordering LDS accesses only: global loads in flight stay in flight across it (a full

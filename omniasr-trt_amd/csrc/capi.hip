@@ -14,4 +14,4 @@ extern "C" const char* omni_status_string(int status) {
   return "unknown status";
 }
 
-extern "C" int omni_abi_version(void) { return 2; }
+extern "C" int omni_abi_version(void) { return 3; }

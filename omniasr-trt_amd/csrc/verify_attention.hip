@@ -66,6 +66,12 @@ struct AttnArgs {
   const int64_t* gen_len = nullptr;
   int gen_cap = 0, gen_rows = 0;
   int gen_table = 0;  // LDS entries of a unit's table of generated-key offsets (a multiple of 32)
+  // Optional: each group's generated keys listed once per distinct (row, position) by beam_gen_list_kernel --
+  // offsets (row and position only), beam masks, lengths; row stride glist_stride.  nullptr: every beam's own keys.
+  const uint32_t* glist = nullptr;
+  const uint16_t* gmask = nullptr;
+  const int32_t* gcount = nullptr;
+  int64_t glist_stride = 0;
 };
 
 struct SplitRange {
@@ -474,6 +480,126 @@ struct BalancedSplit {
   int b, k, nact, first;
 };
 
+// Bit j: whether query c sees key 8g + j of a tile of a generated-key list (its keys' beam masks at msk8, in LDS).
+__device__ __forceinline__ int gen_bits(const uint16_t* msk8, int c) {
+  const u32x4_t m = *reinterpret_cast<const u32x4_t*>(msk8);
+  int bits = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) bits |= (int)((m[j >> 1] >> (16 * (j & 1) + c)) & 1u) << j;
+  return bits;
+}
+
+// A unit's table of generated keys in LDS (group b's ng keys; cnt: its beams' key counts, LDS): the byte offset of
+// key f from the head's base and the beams that see it, padded to whole tiles with the list's last key (a key in use,
+// so the padding reads finite values) seen by none.  With a.glist the keys are the group's list (each distinct (row,
+// position) once); otherwise beam 0's keys, then beam 1's, ... (key j of beam e at row ptr[e, j]).  Every thread of
+// the workgroup (nt of them) calls it; the caller's barrier follows.
+__device__ __forceinline__ void fill_gen_table(const AttnArgs& a, int b, int ng, const int* cnt, uint32_t* tab,
+                                               uint16_t* msk, int nt, int D) {
+  const int T = a.T;
+  for (int f = threadIdx.x; f < ((ng + 31) & ~31); f += nt) {
+    const int ff = f < ng ? f : ng - 1;
+    if (a.glist) {
+      const int64_t at = (int64_t)b * a.glist_stride + ff;
+      tab[f] = a.glist[at];
+      msk[f] = f < ng ? a.gmask[at] : (uint16_t)0;
+      continue;
+    }
+    int e = 0, base = 0;
+    for (; e < T - 1; ++e) {
+      const int ne = cnt[e];
+      if (ff < base + ne) break;
+      base += ne;
+    }
+    const int j = ff - base;
+    const int64_t src = clamp64(a.ptr[(int64_t)(b * T + e) * a.ptr_stride + j], 0, a.gen_rows - 1);
+    tab[f] = (uint32_t)((src * a.g_row + (int64_t)j * D) * 2);
+    msk[f] = f < ng ? (uint16_t)(1u << e) : (uint16_t)0;
+  }
+}
+
+// One workgroup per group: the group's generated keys listed once per distinct (row, position).  Beams share most of
+// their history, so a key several beams reach through their pointers is read once per launch and seen by all of
+// them.  Order: by position, then by the first beam that reaches the key (the same list every call).  list[f]: the
+// byte offset of key f from a generated cache's (layer's) head base, row ptr[r, j] and position j; mask[f]: the beams
+// that see it; count: the list's length.  Thread t lists positions t, t + 256, ...: one round trip for the pointers
+// and one scan per round.  Built once per search step, read by every layer's launch.
+struct GenListArgs {
+  const int32_t* ptr;
+  int64_t ptr_stride;
+  const int64_t* gen_len;
+  int64_t gen_cap, gen_rows, g_row, g_pos;
+  int beams;
+  uint32_t* list;
+  uint16_t* mask;
+  int32_t* count;
+  int64_t stride;
+};
+
+__global__ __launch_bounds__(256) void beam_gen_list_kernel(GenListArgs a) {
+  constexpr int NT = 256, NW = NT / 64, MAXB = kWideMaxBeams;
+  __shared__ int wsum[NW];
+  const int grp = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, T = a.beams;
+  const int32_t* prow = a.ptr + (int64_t)grp * T * a.ptr_stride;
+  // The beams' key counts (the same for every thread) and the first round's pointers load together: a pointer's
+  // address does not depend on the count (positions clamped into the capacity).
+  int cnt[MAXB], raw[MAXB];
+  int longest = 0;
+#pragma unroll
+  for (int e = 0; e < MAXB; ++e) {
+    cnt[e] = e < T ? (int)clamp64(a.gen_len[(int64_t)grp * T + e], 0, a.gen_cap) : 0;
+    raw[e] = e < T ? prow[(int64_t)e * a.ptr_stride + min((int64_t)tid, a.gen_cap - 1)] : 0;
+    longest = max(longest, cnt[e]);
+  }
+  uint32_t* list = a.list + (int64_t)grp * a.stride;
+  uint16_t* mask = a.mask + (int64_t)grp * a.stride;
+  int total = 0;
+  for (int j0 = 0; j0 < longest; j0 += NT) {
+    const int j = j0 + tid;
+    int src[MAXB];
+#pragma unroll
+    for (int e = 0; e < MAXB; ++e) {  // beam e's row for position j (clamped), -1 where the beam has no key j
+      const int p = j0 == 0 ? raw[e] : (e < T && j < cnt[e] ? prow[(int64_t)e * a.ptr_stride + j] : 0);
+      src[e] = e < T && j < cnt[e] ? (int)clamp64(p, 0, a.gen_rows - 1) : -1;
+    }
+    auto first = [&](int e) {  // beam e reaches a key no earlier beam reaches
+      bool f = src[e] >= 0;
+#pragma unroll
+      for (int e2 = 0; e2 < MAXB; ++e2) f &= !(e2 < e && src[e2] == src[e]);
+      return f;
+    };
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < MAXB; ++e) mine += first(e) ? 1 : 0;
+    int incl = mine;  // inclusive scan within the wave, then over the waves' totals
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o, kWave);
+      incl += lane >= o ? v : 0;
+    }
+    if (lane == 63) wsum[wv] = incl;
+    __syncthreads();
+    int f = total + incl - mine;
+    for (int q = 0; q < NW; ++q) {
+      const int x = wsum[q];
+      f += q < wv ? x : 0;
+      total += x;
+    }
+#pragma unroll
+    for (int e = 0; e < MAXB; ++e) {
+      if (!first(e)) continue;
+      uint32_t m = 0;
+#pragma unroll
+      for (int e2 = 0; e2 < MAXB; ++e2) m |= src[e2] == src[e] ? 1u << e2 : 0u;
+      list[f] = (uint32_t)(((int64_t)src[e] * a.g_row + (int64_t)j * a.g_pos) * 2);
+      mask[f] = (uint16_t)m;
+      ++f;
+    }
+    __syncthreads();  // wsum is written again in the next round
+  }
+  if (tid == 0) a.count[grp] = total;
+}
+
 template <bool GEN = false>
 __device__ BalancedSplit balanced_split(const AttnArgs& a, int j, int* gl = nullptr) {
   __shared__ int nt[kBalancedMaxRows], wk[kBalancedMaxRows], rem[kBalancedMaxRows];
@@ -488,7 +614,7 @@ __device__ BalancedSplit balanced_split(const AttnArgs& a, int j, int* gl = null
         gl[tid * a.T + e] = ne;
         ng += ne;
       }
-      n += (ng + 31) >> 5;
+      n += ((a.glist ? a.gcount[tid] : ng) + 31) >> 5;
     }
     nt[tid] = n;
   }
@@ -541,10 +667,10 @@ __device__ BalancedSplit balanced_split(const AttnArgs& a, int j, int* gl = null
 // the same softmax state; each then accumulates its own slice of P V.  Tiles are dealt to the splits as in
 // attend_split; the partials and the last split's merge are those of verify_attn_mfma_kernel.
 //
-// GEN (beams, balanced): a row's tiles are its context tiles followed by its beams' generated keys -- beam 0's, then
-// beam 1's, ... as one list cut into 32-key tiles, key f at the byte offset the workgroup's table in LDS gives (row
-// ptr[r, j] of the generated cache, position j) -- and query (beam) i sees only its own run [P_i, P_i+1) of that
-// list, so the deal, the pipeline and the merge treat the generated keys like any other tile.
+// GEN (beams, balanced): a row's tiles are its context tiles followed by its group's generated keys as one list cut
+// into 32-key tiles -- the step's list of distinct (row, position) keys (a.glist), or beam 0's keys, then beam 1's,
+// ... -- key f at the byte offset the workgroup's table in LDS gives and seen by the beams of its mask, so the deal,
+// the pipeline and the merge treat the generated keys like any other tile.
 template <int D, int G, bool GEN = false>
 __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_slice_kernel(AttnArgs a) {
   constexpr int NSL = D / 128;
@@ -553,6 +679,7 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
   // GEN: the rows' generated-key counts [rows][T] and the unit's table of key offsets
   __shared__ int s_gl[GEN ? kBalancedMaxRows * kWideMaxBeams : 1];
   __shared__ __align__(16) uint32_t s_tab[GEN ? kWideMaxGenTable : 4];
+  __shared__ __align__(16) uint16_t s_msk[GEN ? kWideMaxGenTable : 8];
   const int h = blockIdx.y;
   int sp, b;
   SplitRange r;
@@ -599,43 +726,17 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
   // The split's tiles are k = 0 .. ntot - 1: tile first + k nact of the row.
   const int ctx_tiles = (int)((r.total + 31) >> 5);
   int64_t row_tiles = ctx_tiles;
-  // GEN: query 16u + c's run [glo[u], ghi[u]) of the row's generated keys; the table of their offsets
-  int glo[G], ghi[G];
+  // GEN: the row's generated keys after its context tiles, their offsets and beam masks in LDS
   const char* kgb = nullptr;
   const char* vgb = nullptr;
   if constexpr (GEN) {
     int ng = 0;
     for (int e = 0; e < T; ++e) ng += s_gl[b * T + e];
-    ng = __builtin_amdgcn_readfirstlane(ng);
+    ng = __builtin_amdgcn_readfirstlane(a.glist ? a.gcount[b] : ng);
     row_tiles += (ng + 31) >> 5;
-#pragma unroll
-    for (int u = 0; u < G; ++u) {
-      const int qi = 16 * u + c;
-      int lo = 0, n = 0;
-      for (int e = 0; e < T; ++e) {
-        const int ne = s_gl[b * T + e];
-        lo += e < qi ? ne : 0;
-        n = e == qi ? ne : n;
-      }
-      glo[u] = lo;
-      ghi[u] = lo + n;  // query qi >= T: an empty run
-    }
     kgb = a.kg + h * a.g_head * 2 + sl * 256;
     vgb = a.vg + h * a.g_head * 2 + sl * 256;
-    // Key f (beam e, position j) at its byte offset from the head's base, padded to whole tiles with the row's last
-    // key (a key in use: the padding reads finite values no query sees).
-    for (int f = threadIdx.x; f < ((ng + 31) & ~31); f += 64 * NSL) {
-      const int ff = f < ng ? f : ng - 1;
-      int e = 0, base = 0;
-      for (; e < T - 1; ++e) {
-        const int ne = s_gl[b * T + e];
-        if (ff < base + ne) break;
-        base += ne;
-      }
-      const int j = ff - base;
-      const int64_t src = clamp64(a.ptr[(int64_t)(b * T + e) * a.ptr_stride + j], 0, a.gen_rows - 1);
-      s_tab[f] = (uint32_t)((src * a.g_row + (int64_t)j * D) * 2);
-    }
+    fill_gen_table(a, b, ng, s_gl + b * T, s_tab, s_msk, 64 * NSL, D);
     __syncthreads();
   }
   const int64_t first = sp;
@@ -682,9 +783,9 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
         }
       }
       const int ti = (int)(first + k * r.nact);
-      if (GEN && ti >= ctx_tiles)  // generated keys: query 16u + c's own run of the list
-        attend_scored<128, true>(t, tot, a.scale_log2, st[u], o[u], g, (ti - ctx_tiles) * 32 + 8 * g - glo[u],
-                                 ghi[u] - glo[u]);
+      if (GEN && ti >= ctx_tiles)  // generated keys: the beams that see each key
+        attend_scored<128, true>(t, tot, a.scale_log2, st[u], o[u], g, 0,
+                                 u == 0 ? gen_bits(s_msk + (ti - ctx_tiles) * 32 + 8 * g, c) : 0);
       else
         attend_scored<128>(t, tot, a.scale_log2, st[u], o[u], g, ti * 32 + 8 * g, lim_c[u]);
     }
@@ -889,7 +990,8 @@ constexpr int kTicketFirst = 1, kTicketClaim = 2, kTicketSecond = 4;
 // with generated keys (beams) also every row's generated-key count and the two units' tables of key offsets.
 __host__ __device__ constexpr size_t pair_lds_bytes(int T, int D, int rows = 0, int gen_table = 0) {
   return (size_t)(kWgWaves + 2) * T * (D + 2) * sizeof(float) + (size_t)T * D * 2 +
-         (((size_t)rows * T + 3) / 4 * 4 + 2 * (size_t)gen_table) * sizeof(int32_t);
+         (((size_t)rows * T + 3) / 4 * 4 + 2 * (size_t)gen_table) * sizeof(int32_t) +
+         2 * (size_t)gen_table * sizeof(uint16_t);
 }
 
 // One 8-wave workgroup per (head, row) unit, working on halves: units are ranked by length, and workgroup i takes
@@ -904,10 +1006,10 @@ __host__ __device__ constexpr size_t pair_lds_bytes(int T, int D, int rows = 0, 
 // fetches it into LDS while the other waves finish, so the common end is an LDS merge and the output store.  The
 // dealing is static, so results do not depend on timing.
 //
-// GEN (beams): each unit's tiles are its context tiles followed by its beams' generated keys -- beam 0's, then beam
-// 1's, ... as one list cut into 32-key tiles, key f at the byte offset the workgroup's table in LDS gives (row
-// ptr[r, j] of the generated cache, position j) -- and query (beam) i sees only its own run [P_i, P_i+1) of that list,
-// so the halves deal, the pipeline and the merges treat the generated keys like any other tile.
+// GEN (beams): each unit's tiles are its context tiles followed by its group's generated keys as one list cut into
+// 32-key tiles -- the step's list of distinct (row, position) keys (a.glist), or beam 0's keys, then beam 1's, ... --
+// key f at the byte offset the workgroup's table in LDS gives and seen by the beams of its mask, so the halves deal,
+// the pipeline and the merges treat the generated keys like any other tile.
 template <int D, bool GEN = false>
 __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(AttnArgs a, int rows, int slots) {
   static_assert(D == 128, "the halves kernel serves head dim 128");
@@ -925,6 +1027,7 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
   // GEN: every row's generated-key counts [rows][T], then the two units' offset tables, after half 1's queries
   int* s_gl = reinterpret_cast<int*>(smem + (kWgWaves + 2) * T * (D + 2) + T * D / 2);
   uint32_t* tab = reinterpret_cast<uint32_t*>(s_gl + ((rows * T + 3) & ~3));  // 16-byte aligned (row reads)
+  uint16_t* msk = reinterpret_cast<uint16_t*>(tab + 2 * a.gen_table);
   if (tid == 0) s_done = 0;
   for (int b = tid; b < rows; b += 64 * kWgWaves) {
     int nt = row_tile_count(a, b);
@@ -935,7 +1038,7 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
         s_gl[b * T + e] = n;
         ng += n;
       }
-      nt += (ng + 31) >> 5;
+      nt += ((a.glist ? a.gcount[b] : ng) + 31) >> 5;
     }
     ntl[b] = nt;
   }
@@ -953,11 +1056,11 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
   const int b0 = u0 / H, h0 = u0 - b0 * H, b1 = u1 / H, h1 = u1 - b1 * H;
   const SplitRange r0 = split_range(a, b0, 0), r1 = split_range(a, b1, 0);
   const int nc0 = (int)((r0.total + 31) >> 5), nc1 = (int)((r1.total + 31) >> 5);  // context tiles
-  // GEN: the units' generated keys (wave-uniform) and, for this lane's query c, its run [glo, ghi) of them
+  // GEN: the units' generated keys (wave-uniform)
   auto gen_total = [&](int bu) {
     int n = 0;
     for (int e = 0; e < T; ++e) n += s_gl[bu * T + e];
-    return __builtin_amdgcn_readfirstlane(n);
+    return __builtin_amdgcn_readfirstlane(a.glist ? a.gcount[bu] : n);
   };
   const int ng0 = GEN ? gen_total(b0) : 0, ng1 = GEN ? gen_total(b1) : 0;
   const int nt0 = nc0 + ((ng0 + 31) >> 5), nt1 = nc1 + ((ng1 + 31) >> 5);
@@ -989,44 +1092,17 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
 #pragma unroll
     for (int s = 0; s < KS; ++s) qop[s] = c < T ? *reinterpret_cast<const u32x4_t*>(qrow + s * 32) : zero;
   }
-  int glo = 0, ghi = 0;
-  auto gen_bounds = [&](int bu) {  // query c >= T: an empty run
-    int lo = 0, n = 0;
-    for (int e = 0; e < T; ++e) {
-      const int ne = s_gl[bu * T + e];
-      lo += e < c ? ne : 0;
-      n = e == c ? ne : n;
-    }
-    glo = lo;
-    ghi = lo + n;
-  };
   const char* kgb0 = nullptr;
   const char* vgb0 = nullptr;
   const char* kgb1 = nullptr;
   const char* vgb1 = nullptr;
   if constexpr (GEN) {
-    gen_bounds(b0);
     kgb0 = a.kg + h0 * a.g_head * 2;
     vgb0 = a.vg + h0 * a.g_head * 2;
     kgb1 = a.kg + h1 * a.g_head * 2;
     vgb1 = a.vg + h1 * a.g_head * 2;
-    // The two units' tables: the byte offset of generated key f (beam e, position j) from the head's base, padded
-    // to whole tiles with the unit's last key (a key in use, so the padding reads finite values no query sees).
-    for (int sel = 0; sel < 2; ++sel) {
-      const int bu = sel ? b1 : b0, ngu = sel ? ng1 : ng0;
-      for (int f = tid; f < ((ngu + 31) & ~31); f += 64 * kWgWaves) {
-        const int ff = f < ngu ? f : ngu - 1;
-        int e = 0, base = 0;
-        for (; e < T - 1; ++e) {
-          const int ne = s_gl[bu * T + e];
-          if (ff < base + ne) break;
-          base += ne;
-        }
-        const int j = ff - base;
-        const int64_t src = clamp64(a.ptr[(int64_t)(bu * T + e) * a.ptr_stride + j], 0, a.gen_rows - 1);
-        tab[sel * a.gen_table + f] = (uint32_t)((src * a.g_row + (int64_t)j * D) * 2);
-      }
-    }
+    fill_gen_table(a, b0, ng0, s_gl + b0 * T, tab, msk, 64 * kWgWaves, D);
+    fill_gen_table(a, b1, ng1, s_gl + b1 * T, tab + a.gen_table, msk + a.gen_table, 64 * kWgWaves, D);
     __syncthreads();
   }
 
@@ -1132,14 +1208,19 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
     for (int s = 0; s < KS; ++s)
       qop[s] = c < T ? *reinterpret_cast<const u32x4_t*>(qs1 + c * D + s * 32 + g * 8) : zero;
     lim = key_limit(r1);
-    if constexpr (GEN) gen_bounds(b1);
   };
   auto at = [&](const KVTile<D>& t, int k) {
     const int tile = tile_of(k);
     if constexpr (GEN) {
-      const int nc = k < n0 ? nc0 : nc1;
-      const bool gt = tile >= nc;  // generated keys: query c's own run of the list
-      attend_range<D>(t, qop, c_scale, st, o, g, (gt ? tile - nc : tile) * 32 + 8 * g, gt ? glo : 0, gt ? ghi : lim);
+      const bool first = k < n0;
+      const int nc = first ? nc0 : nc1;
+      const bool gt = tile >= nc;  // generated keys: the beams that see each key; context: the key limit
+      // the masks are read on every tile (a clamped index), so that no load waits under a branch
+      const int gb = gen_bits(msk + (first ? 0 : a.gen_table) + (gt ? tile - nc : 0) * 32 + 8 * g, c);
+      int cb = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cb |= tile * 32 + 8 * g + j < lim ? 1 << j : 0;
+      attend_bits<D>(t, qop, c_scale, st, o, g, gt ? gb : cb);
     } else {
       attend<D>(t, qop, c_scale, st, o, g, tile * 32 + 8 * g, lim);
     }
@@ -2108,15 +2189,44 @@ extern "C" size_t omni_beam_attention_workspace(int32_t groups, int32_t beams, i
   return align256(units * head_dim * sizeof(float)) + align256(units * 2 * sizeof(float));
 }
 
-extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void* v_ctx, int64_t ctx_row,
-                                   int64_t ctx_head, int64_t ctx_pos, int64_t ctx_cap, const int64_t* ctx_len,
-                                   const void* k_gen, const void* v_gen, int64_t gen_row, int64_t gen_head,
-                                   int64_t gen_pos, int64_t gen_cap, int64_t gen_rows, const int32_t* ptr,
-                                   int64_t ptr_stride, const int64_t* gen_len, int32_t groups, int32_t beams,
-                                   int32_t heads, int32_t head_dim, int32_t ctx_keys, int32_t chunk, float scale,
-                                   void* out, void* workspace, size_t workspace_bytes, int32_t* counters,
-                                   int32_t dtype, void* stream) {
+extern "C" int omni_beam_gen_list(int32_t groups, int32_t beams, const int32_t* ptr, int64_t ptr_stride,
+                                  const int64_t* gen_len, int64_t gen_cap, int64_t gen_rows, int64_t gen_row,
+                                  int64_t gen_pos, uint32_t* list, uint16_t* mask, int32_t* count, int64_t list_stride,
+                                  void* stream) {
+  if (groups < 0 || beams < 1 || beams > kWideMaxBeams || gen_cap <= 0 || gen_rows <= 0) return OMNI_ERR_INVALID;
+  if (groups == 0) return OMNI_OK;
+  if (!ptr || !gen_len || !list || !mask || !count || ptr_stride < gen_cap || list_stride < beams * gen_cap)
+    return OMNI_ERR_INVALID;
+  if (gen_row < 0 || gen_pos < 0 || ((gen_rows - 1) * gen_row + (gen_cap - 1) * gen_pos) * 2 > (int64_t)UINT32_MAX)
+    return OMNI_ERR_SHAPE;  // byte offsets of 32 bits
+  GenListArgs a;
+  a.ptr = ptr;
+  a.ptr_stride = ptr_stride;
+  a.gen_len = gen_len;
+  a.gen_cap = gen_cap;
+  a.gen_rows = gen_rows;
+  a.g_row = gen_row;
+  a.g_pos = gen_pos;
+  a.beams = beams;
+  a.list = list;
+  a.mask = mask;
+  a.count = count;
+  a.stride = list_stride;
+  beam_gen_list_kernel<<<groups, 256, 0, (hipStream_t)stream>>>(a);
+  return omni_launch_status();
+}
+
+static int beam_attention(const void* q, const void* k_ctx, const void* v_ctx, int64_t ctx_row, int64_t ctx_head,
+                          int64_t ctx_pos, int64_t ctx_cap, const int64_t* ctx_len, const void* k_gen,
+                          const void* v_gen, int64_t gen_row, int64_t gen_head, int64_t gen_pos, int64_t gen_cap,
+                          int64_t gen_rows, const int32_t* ptr, int64_t ptr_stride, const int64_t* gen_len,
+                          const uint32_t* gen_list, const uint16_t* gen_mask, const int32_t* gen_count,
+                          int64_t list_stride, int32_t groups, int32_t beams, int32_t heads, int32_t head_dim,
+                          int32_t ctx_keys, int32_t chunk, float scale, void* out, void* workspace,
+                          size_t workspace_bytes, int32_t* counters, int32_t dtype, void* stream) {
   if (groups < 0 || ctx_keys <= 0 || ctx_cap <= 0 || gen_cap <= 0 || gen_rows <= 0) return OMNI_ERR_INVALID;
+  const bool listed = gen_list != nullptr;
+  if (listed && (!gen_mask || !gen_count || list_stride < (int64_t)beams * gen_cap)) return OMNI_ERR_INVALID;
   int st = check_attention_shape(beams, heads, head_dim, dtype, scale, 0);  // beams: 1..16
   if (st != OMNI_OK) return st;
   if (groups == 0) return OMNI_OK;
@@ -2188,6 +2298,12 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
     a.gen_cap = (int)gen_cap;
     a.gen_rows = (int)gen_rows;
     a.gen_table = (int)table;
+    if (listed) {  // each group's keys once per distinct (row, position): at most beams x gen_cap of them
+      a.glist = gen_list;
+      a.gmask = gen_mask;
+      a.gcount = gen_count;
+      a.glist_stride = list_stride;
+    }
   };
   if (halves) {  // the generated keys' partial first, then the context halves, whose last merge includes it
     a.chunk = (ctx_keys + 31) / 32 * 32;
@@ -2254,4 +2370,34 @@ extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void*
     return omni_launch_status();
   }
   return launch_combine(a, groups, dtype, s);
+}
+
+extern "C" int omni_beam_attention(const void* q, const void* k_ctx, const void* v_ctx, int64_t ctx_row,
+                                   int64_t ctx_head, int64_t ctx_pos, int64_t ctx_cap, const int64_t* ctx_len,
+                                   const void* k_gen, const void* v_gen, int64_t gen_row, int64_t gen_head,
+                                   int64_t gen_pos, int64_t gen_cap, int64_t gen_rows, const int32_t* ptr,
+                                   int64_t ptr_stride, const int64_t* gen_len, int32_t groups, int32_t beams,
+                                   int32_t heads, int32_t head_dim, int32_t ctx_keys, int32_t chunk, float scale,
+                                   void* out, void* workspace, size_t workspace_bytes, int32_t* counters,
+                                   int32_t dtype, void* stream) {
+  return beam_attention(q, k_ctx, v_ctx, ctx_row, ctx_head, ctx_pos, ctx_cap, ctx_len, k_gen, v_gen, gen_row, gen_head,
+                        gen_pos, gen_cap, gen_rows, ptr, ptr_stride, gen_len, nullptr, nullptr, nullptr, 0, groups,
+                        beams, heads, head_dim, ctx_keys, chunk, scale, out, workspace, workspace_bytes, counters, dtype,
+                        stream);
+}
+
+extern "C" int omni_beam_attention_listed(const void* q, const void* k_ctx, const void* v_ctx, int64_t ctx_row,
+                                          int64_t ctx_head, int64_t ctx_pos, int64_t ctx_cap, const int64_t* ctx_len,
+                                          const void* k_gen, const void* v_gen, int64_t gen_row, int64_t gen_head,
+                                          int64_t gen_pos, int64_t gen_cap, int64_t gen_rows, const int32_t* ptr,
+                                          int64_t ptr_stride, const int64_t* gen_len, const uint32_t* gen_list,
+                                          const uint16_t* gen_mask, const int32_t* gen_count, int64_t list_stride,
+                                          int32_t groups, int32_t beams, int32_t heads, int32_t head_dim,
+                                          int32_t ctx_keys, int32_t chunk, float scale, void* out, void* workspace,
+                                          size_t workspace_bytes, int32_t* counters, int32_t dtype, void* stream) {
+  if (!gen_list) return OMNI_ERR_INVALID;
+  return beam_attention(q, k_ctx, v_ctx, ctx_row, ctx_head, ctx_pos, ctx_cap, ctx_len, k_gen, v_gen, gen_row, gen_head,
+                        gen_pos, gen_cap, gen_rows, ptr, ptr_stride, gen_len, gen_list, gen_mask, gen_count,
+                        list_stride, groups, beams, heads, head_dim, ctx_keys, chunk, scale, out, workspace,
+                        workspace_bytes, counters, dtype, stream);
 }

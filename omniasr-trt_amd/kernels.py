@@ -231,13 +231,47 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
                    ATTN["separate"], ATTN["split_k"])
 
 
+class GenList:
+    """Each group's generated keys listed once per distinct (row, position) -- ``offsets`` [S, N*G] uint32 (as
+    int32), ``masks`` [S, N*G] uint16 (as int16), ``counts`` [S] int32 -- built by :func:`beam_gen_list` from one
+    step's pointers and lengths for generated caches of one layout; :func:`beam_attention` reads it."""
+
+    def __init__(self, groups: int, beams: int, gen_cap: int, device):
+        self.stride = beams * gen_cap
+        self.offsets = torch.empty(groups, self.stride, dtype=torch.int32, device=device)
+        self.masks = torch.empty(groups, self.stride, dtype=torch.int16, device=device)
+        self.counts = torch.zeros(groups, dtype=torch.int32, device=device)
+        self.groups, self.beams, self.gen_cap = groups, beams, gen_cap
+        self.layout = None  # (strides, rows) of the generated caches the offsets address
+
+
+def beam_gen_list(lst: GenList, ptr: torch.Tensor, gen_len: torch.Tensor, kg: torch.Tensor, groups: int) -> GenList:
+    """Fill ``lst`` for groups 0..groups-1 from ``ptr`` [>=S*N, >=G] int32 and ``gen_len`` [>=S*N] (as for
+    :func:`beam_attention`), for generated caches laid out as ``kg`` [rows, H, G, D] (every layer's cache of one
+    decoder shares the layout).  One launch; the beams of a group share most generated keys, and the attention then
+    reads each of them once.  No counterpart in the reference."""
+    lib = _lib.load()
+    _need(0 < groups <= lst.groups and kg.size(2) == lst.gen_cap, "list: groups and generated capacity")
+    _need(ptr.dtype == torch.int32 and ptr.dim() == 2 and ptr.stride(1) == 1 and ptr.size(1) >= kg.size(2),
+          "ptr: [>=S*N, >=G] int32 with unit stride in positions")
+    _index(gen_len, "gen_len")
+    _need(ptr.size(0) >= groups * lst.beams and gen_len.numel() >= groups * lst.beams, "ptr / gen_len: S*N rows")
+    status = lib.omni_beam_gen_list(groups, lst.beams, ptr.data_ptr(), ptr.stride(0), gen_len.data_ptr(), kg.size(2),
+                                    kg.size(0), kg.stride(0), kg.stride(2), lst.offsets.data_ptr(),
+                                    lst.masks.data_ptr(), lst.counts.data_ptr(), lst.stride, _stream(kg))
+    _lib.check(status, "beam generated-key list")
+    lst.layout = (kg.stride(), kg.size(0))
+    return lst
+
+
 def beam_attention(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, ctx_len: torch.Tensor, kg: torch.Tensor,
                    vg: torch.Tensor, ptr: torch.Tensor, gen_len: torch.Tensor, beams: int, ctx_keys: int,
-                   scale: float, chunk: int = 0) -> torch.Tensor:
+                   scale: float, chunk: int = 0, gen_list: GenList | None = None) -> torch.Tensor:
     """Beam rows ``q`` [S*N, H, D] (input g's beams are rows g*N .. g*N+N-1): attention over input g's context
     ``kc``/``vc`` [>=S, H, C, D] (first ``ctx_len[g]`` keys, all within ``ctx_keys``) and row r's generated keys
     ``kg``/``vg`` [>=S*N, H, G, D], position j read from row ``ptr[r, j]`` (first ``gen_len[r]``).  One pass over
-    a group's context serves all of its beams.  Returns [S*N, H, D] in q's dtype.
+    a group's context serves all of its beams.  Returns [S*N, H, D] in q's dtype.  ``gen_list``: the step's
+    :func:`beam_gen_list` of the same pointers and lengths (optional; each shared generated key is then read once).
     (src/omniasr_trt/kernels.py:309-332)"""
     lib = _lib.load()
     rows, heads, dim = q.shape
@@ -260,12 +294,18 @@ def beam_attention(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, ctx_len:
     workspace = torch.empty(max(ws, 256), device=q.device, dtype=torch.uint8)
     counters = _attn_counters(q.device, groups * heads)
     out = torch.empty_like(q)
-    status = lib.omni_beam_attention(
-        q.data_ptr(), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.size(2),
-        ctx_len.data_ptr(), kg.data_ptr(), vg.data_ptr(), kg.stride(0), kg.stride(1), kg.stride(2), kg.size(2),
-        kg.size(0), ptr.data_ptr(), ptr.stride(0), gen_len.data_ptr(), groups, beams, heads, dim, int(ctx_keys),
-        int(chunk), float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel(), counters.data_ptr(),
-        _dtype(q), _stream(q))
+    args = (q.data_ptr(), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.size(2),
+            ctx_len.data_ptr(), kg.data_ptr(), vg.data_ptr(), kg.stride(0), kg.stride(1), kg.stride(2), kg.size(2),
+            kg.size(0), ptr.data_ptr(), ptr.stride(0), gen_len.data_ptr())
+    tail = (groups, beams, heads, dim, int(ctx_keys), int(chunk), float(scale), out.data_ptr(), workspace.data_ptr(),
+            workspace.numel(), counters.data_ptr(), _dtype(q), _stream(q))
+    if gen_list is None:
+        status = lib.omni_beam_attention(*args, *tail)
+    else:
+        _need(gen_list.beams == beams and gen_list.groups >= groups and gen_list.layout == (kg.stride(), kg.size(0)),
+              "gen_list: built by beam_gen_list for these beams and generated caches")
+        status = lib.omni_beam_attention_listed(*args, gen_list.offsets.data_ptr(), gen_list.masks.data_ptr(),
+                                                gen_list.counts.data_ptr(), gen_list.stride, *tail)
     _lib.check(status, "beam attention")
     return out
 

@@ -6,8 +6,8 @@ kernel's inputs recorded and checked:
 * the bookkeeping before the layers (``beam_prepare``) equals ``oracle.verify.beam_prepare`` on the state before the
   step (positions, generated positions, key counts, the rows' own pointers);
 * in the first and the last layer, ``beam_attention`` (the context by the halves kernel with the beams as queries,
-  the generated keys through the pointers) equals ``oracle.verify.beam_attention`` on the same inputs within the bf16
-  bound (2e-2 abs / 1e-2 rel);
+  the generated keys as tiles of the same launch, each distinct (row, position) once from the step's list) equals
+  ``oracle.verify.beam_attention`` on the same inputs within the bf16 bound (2e-2 abs / 1e-2 rel);
 * the choice (torch's log-softmax, then the offers and top-k in one launch) equals the choice made on torch's own ops
   over the same logits and state (src/omniasr_trt/beam.py:162-175), indices and values bit for bit;
 * the bookkeeping after the top-k (``beam_take_over``) leaves exactly the state ``oracle.verify.beam_take_over``
@@ -71,8 +71,9 @@ def test_config5_beam_steps(cuda, monkeypatch):
         real_prepare(groups, beams, ctx, k_step, group_done, ptr, *out)
         rec["prepare_out"] = [host(t) for t in out] + [host(ptr)]
 
-    def attention(q, kc, vc, ctx_len, kg, vg, ptr, gen_len, beams, ctx_keys, scale, chunk=0):
-        out = real_attn(q, kc, vc, ctx_len, kg, vg, ptr, gen_len, beams, ctx_keys, scale, chunk)
+    def attention(q, kc, vc, ctx_len, kg, vg, ptr, gen_len, beams, ctx_keys, scale, chunk=0, gen_list=None):
+        assert gen_list is not None  # bf16: the step's list of distinct generated keys
+        out = real_attn(q, kc, vc, ctx_len, kg, vg, ptr, gen_len, beams, ctx_keys, scale, chunk, gen_list)
         i = rec["layer"]
         rec["layer"] += 1
         if i in (0, layers - 1):

@@ -138,6 +138,112 @@ def test_beam_attention_long_generation(cuda, h, d):
     assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
 
 
+def _shared_pointers(groups, beams, gcap, rows, seed, share=0.85):
+    """Pointers like a beam search's: at each position the beams of a group mostly reach one row (a shared
+    history), sometimes their own, and a few out of range (clamped by the kernels)."""
+    g = np.random.default_rng(seed)
+    ptr = np.zeros((groups * beams, gcap), dtype=np.int32)
+    for grp in range(groups):
+        common = g.integers(0, rows, gcap)
+        for e in range(beams):
+            own = g.integers(0, rows, gcap)
+            ptr[grp * beams + e] = np.where(g.random(gcap) < share, common, own)
+    ptr[0, :3] = [-4, rows + 7, rows - 1]
+    return torch.as_tensor(ptr)
+
+
+def _list_reference(ptr, gen_len, groups, beams, gcap, rows, g_row, g_pos):
+    """Each group's distinct (row, position) keys: by position, then by the first beam that reaches the key; the
+    byte offset (row * g_row + position * g_pos) * 2 and the mask of the beams that see it."""
+    out = []
+    for grp in range(groups):
+        n = [int(np.clip(gen_len[grp * beams + e], 0, gcap)) for e in range(beams)]
+        offs, masks = [], []
+        for j in range(max(n)):
+            src = [int(np.clip(ptr[grp * beams + e, j], 0, rows - 1)) if j < n[e] else -1 for e in range(beams)]
+            for e in range(beams):
+                if src[e] < 0 or src[e] in src[:e]:
+                    continue
+                offs.append((src[e] * g_row + j * g_pos) * 2)
+                masks.append(sum(1 << e2 for e2 in range(beams) if src[e2] == src[e]))
+        out.append((offs, masks))
+    return out
+
+
+@pytest.mark.parametrize("beams,d", [(5, 128), (16, 512), (1, 128)])
+def test_beam_gen_list(cuda, beams, d):
+    """kernels.beam_gen_list: every group's distinct generated keys with the beams that see each, in position
+    order, against the list restated in Python -- ragged and empty generations, clamped pointers, 16 beams."""
+    groups, gcap, h = 6, 160, 2
+    rows = groups * beams
+    kg = torch.empty(rows + 2, h, gcap, d, dtype=torch.bfloat16, device=cuda)
+    ptr = _shared_pointers(groups, beams, gcap, rows + 2, 7 + beams)
+    gen_len = torch.randint(0, gcap + 1, (rows,), generator=torch.Generator().manual_seed(beams))
+    gen_len[beams: 2 * beams] = 0
+    gen_len[0] = gcap
+    lst = kernels.GenList(groups, beams, gcap, cuda)
+    kernels.beam_gen_list(lst, ptr.to(cuda), gen_len.to(cuda), kg, groups)
+    torch.cuda.synchronize()
+    want = _list_reference(ptr.numpy(), gen_len.numpy(), groups, beams, gcap, rows + 2, kg.stride(0), kg.stride(2))
+    offs = lst.offsets.cpu().numpy().view(np.uint32)
+    masks = lst.masks.cpu().numpy().view(np.uint16)
+    counts = lst.counts.cpu().numpy()
+    for grp, (w_off, w_mask) in enumerate(want):
+        assert counts[grp] == len(w_off), grp
+        np.testing.assert_array_equal(offs[grp, :counts[grp]], np.array(w_off, dtype=np.uint32), err_msg=str(grp))
+        np.testing.assert_array_equal(masks[grp, :counts[grp]], np.array(w_mask, dtype=np.uint16), err_msg=str(grp))
+    total = int(sum(min(int(x), gcap) for x in gen_len))
+    say(f"beam_gen_list beams={beams}: {total} generated keys, {int(counts.sum())} distinct")
+    if beams > 1:
+        assert counts.sum() < total / 2  # the beams share most keys
+
+
+@pytest.mark.parametrize("h,d", [(32, 128), (8, 512)])
+def test_beam_attention_with_gen_list(cuda, h, d):
+    """Both context kernels with the step's list of distinct generated keys: against the oracle and against the
+    same call without the list, pointers shared like a beam search's, ragged generations, a finished input, an input
+    with generated keys only; then captured in a graph with the list's build and replayed with new pointers and
+    lengths, every replay equal to the eager calls bit for bit; the tickets are left zero."""
+    groups, beams, gcap = 8, 5, 128
+    rows = groups * beams
+    ctx_len = torch.tensor([2000, 0, 333, 1500, 0, 900, 64, 1200])
+    gen_len = torch.randint(0, gcap + 1, (rows,), generator=torch.Generator().manual_seed(h))
+    gen_len[5:10] = 0  # input 1 finished
+    q, kc, vc, kg, vg, _, cl, gl = _beam_inputs(torch.bfloat16, groups, beams, h, d, 2048, gcap, ctx_len, gen_len, 31)
+    ptr = _shared_pointers(groups, beams, gcap, rows + 2, 32)
+    want = ov.beam_attention(npf(q), npf(kc), npf(vc), cl.numpy(), npf(kg), npf(vg), ptr.numpy(), gl.numpy(), beams,
+                             d ** -0.5)
+    q, kc, vc, kg, vg, ptr, cl, gl = (t.to(cuda) for t in (q, kc, vc, kg, vg, ptr, cl, gl))
+    lst = kernels.GenList(groups, beams, gcap, cuda)
+    kernels.beam_gen_list(lst, ptr, gl, kg, groups)
+    got = kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr, gl, beams, 2048, d ** -0.5, gen_list=lst)
+    plain = kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr, gl, beams, 2048, d ** -0.5)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(npf(got), want, atol=BF16_TOL[0], rtol=BF16_TOL[1])
+    torch.testing.assert_close(got.float(), plain.float(), atol=1e-2, rtol=1e-2)
+    assert torch.all(got[5:10] == 0)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        graph.capture_begin()
+        kernels.beam_gen_list(lst, ptr, gl, kg, groups)
+        out = kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr, gl, beams, 2048, d ** -0.5, gen_list=lst)
+        graph.capture_end()
+    torch.cuda.current_stream().wait_stream(stream)
+    for rep in range(3):
+        ptr.copy_(_shared_pointers(groups, beams, gcap, rows + 2, 40 + rep).to(cuda))
+        gl.copy_(torch.randint(0, gcap + 1, (rows,), generator=torch.Generator().manual_seed(50 + rep)).to(cuda))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        kernels.beam_gen_list(lst, ptr, gl, kg, groups)
+        eager = kernels.beam_attention(q, kc, vc, cl, kg, vg, ptr, gl, beams, 2048, d ** -0.5, gen_list=lst)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), rep
+    assert int(kernels._counters[torch.cuda.current_device()].abs().sum()) == 0
+
+
 @pytest.mark.parametrize("beams", [1, 5, 16])
 def test_beam_attention_wide_balanced(cuda, beams):
     """8 inputs x 8 heads x 512 (the real checkpoint's shape): the balanced wide-head kernel with each input's
