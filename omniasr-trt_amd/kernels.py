@@ -11,7 +11,9 @@ through its C ABI (``include/omniasr_mi355x.h``) on torch's current stream:
   its one-query case (``omni_verify_attention``);
 * :func:`propose` -- the draft proposal of every row (``omni_propose``);
 * :func:`accept` -- greedy acceptance and rollback (``omni_accept``);
-* :func:`beam_attention` -- beam search's shared-context plus generated-keys attention (``omni_beam_attention``).
+* :func:`beam_attention` -- beam search's shared-context plus generated-keys attention (``omni_beam_attention``);
+  with a :class:`GenList` from :func:`beam_gen_list` (no counterpart in the reference) each generated key the beams
+  of a group share is read once (``omni_beam_gen_list``, ``omni_beam_attention_listed``).
 
 Beyond the reference's functions, for the fused step: :func:`spec_prepare` (proposal plus the step's
 tokens / positions / cache rows / key counts in one launch) and :func:`greedy_accept` (the argmax of
