@@ -614,7 +614,7 @@ __device__ BalancedSplit balanced_split(const AttnArgs& a, int j, int* gl = null
         gl[tid * a.T + e] = ne;
         ng += ne;
       }
-      n += ((a.glist ? a.gcount[tid] : ng) + 31) >> 5;
+      n += ((a.glist ? min(a.gcount[tid], a.gen_table) : ng) + 31) >> 5;
     }
     nt[tid] = n;
   }
@@ -732,7 +732,7 @@ __global__ __launch_bounds__(64 * (D / 128), G == 1 ? 2 : 1) void verify_attn_sl
   if constexpr (GEN) {
     int ng = 0;
     for (int e = 0; e < T; ++e) ng += s_gl[b * T + e];
-    ng = __builtin_amdgcn_readfirstlane(a.glist ? a.gcount[b] : ng);
+    ng = __builtin_amdgcn_readfirstlane(a.glist ? min(a.gcount[b], a.gen_table) : ng);  // a list holds at most the table
     row_tiles += (ng + 31) >> 5;
     kgb = a.kg + h * a.g_head * 2 + sl * 256;
     vgb = a.vg + h * a.g_head * 2 + sl * 256;
@@ -1038,7 +1038,7 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
         s_gl[b * T + e] = n;
         ng += n;
       }
-      nt += ((a.glist ? a.gcount[b] : ng) + 31) >> 5;
+      nt += ((a.glist ? min(a.gcount[b], a.gen_table) : ng) + 31) >> 5;
     }
     ntl[b] = nt;
   }
@@ -1060,7 +1060,7 @@ __global__ __launch_bounds__(64 * kWgWaves, 1) void verify_attn_pair_kernel(Attn
   auto gen_total = [&](int bu) {
     int n = 0;
     for (int e = 0; e < T; ++e) n += s_gl[bu * T + e];
-    return __builtin_amdgcn_readfirstlane(a.glist ? a.gcount[bu] : n);
+    return __builtin_amdgcn_readfirstlane(a.glist ? min(a.gcount[bu], a.gen_table) : n);  // at most the table
   };
   const int ng0 = GEN ? gen_total(b0) : 0, ng1 = GEN ? gen_total(b1) : 0;
   const int nt0 = nc0 + ((ng0 + 31) >> 5), nt1 = nc1 + ((ng1 + 31) >> 5);
