@@ -161,7 +161,7 @@ class BeamDecoder(GreedyDecoder):
             def attend(qkv, i=i, kg=kg, vg=vg):
                 q = kernels.rope_kv(qkv, self.m.rope, pos, kg, vg, self.heads, None, gen_pos)
                 return kernels.beam_attention(q, self.kc[i], self.vc[i], ctx_len, kg, vg, ptr, gen_len, n, ckeys,
-                                              scale, gen_list=lst).reshape(r, -1)
+                                              scale, gen_list=lst, tickets=self.attn_tickets).reshape(r, -1)
 
             self._layer(i, h, attend)
         logits = self._head(h)  # [R, V]

@@ -111,6 +111,9 @@ class GreedyDecoder:
         self.tok = torch.zeros(rows, dtype=torch.long, device=dev)
         self.last = torch.zeros(rows, dtype=torch.long, device=dev)
         self.done = torch.ones(rows, dtype=torch.bool, device=dev)
+        # This decoder's own merge tickets of the attention (one per (row, head), zero between launches), so that
+        # two decoders on different streams of one GPU never share them.
+        self.attn_tickets = torch.zeros(rows * self.heads, dtype=torch.int32, device=dev)
 
     # ------------------------------------------------------------------ slot state kept across steps and graphs
 
@@ -219,7 +222,8 @@ class GreedyDecoder:
 
             def attend(qkv, kc=kc, vc=vc):
                 q = kernels.rope_kv(qkv, self.m.rope, pos, kc, vc, self.heads, slots)
-                return kernels.draft_attention(q, kc, vc, lengths, tokens, keys, scale).reshape(n, -1)
+                return kernels.draft_attention(q, kc, vc, lengths, tokens, keys, scale,
+                                               tickets=self.attn_tickets).reshape(n, -1)
 
             self._layer(i, h, attend)
         return self._head(h)

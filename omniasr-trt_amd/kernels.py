@@ -134,8 +134,20 @@ def _attn_counters(device: torch.device, n: int) -> torch.Tensor:
     return _tickets(_counters, device, n, "verify attention", 1 << 16)
 
 
+def _own_tickets(tickets: torch.Tensor | None, device: torch.device, n: int) -> torch.Tensor:
+    """A caller's merge tickets (zero, at least ``n`` int32 on ``device``, left zero by every call), or the shared
+    per-device ones.  Calls that share tickets must not overlap in time: a caller that runs on its own stream beside
+    others (each decoder) passes its own."""
+    if tickets is None:
+        return _attn_counters(device, n)
+    _need(tickets.dtype == torch.int32 and tickets.is_contiguous() and tickets.device == device
+          and tickets.numel() >= n, f"tickets: at least {n} contiguous int32 on {device}")
+    return tickets
+
+
 def _verify(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor, tokens: int,
-            keys: int, scale: float, chunk: int, separate: bool, split_k: bool = False) -> torch.Tensor:
+            keys: int, scale: float, chunk: int, separate: bool, split_k: bool = False,
+            tickets: torch.Tensor | None = None) -> torch.Tensor:
     lib = _lib.load()
     rows_total, heads, dim = q.shape
     _need(rows_total % tokens == 0, "q: [B*T, H, D]")
@@ -150,7 +162,7 @@ def _verify(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengt
     chunk = int(chunk or 0)
     ws = lib.omni_verify_attention_workspace(groups, tokens, heads, dim, keys, chunk)
     workspace = torch.empty(max(ws, 256), device=q.device, dtype=torch.uint8)
-    counters = _attn_counters(q.device, groups * heads)
+    counters = _own_tickets(tickets, q.device, groups * heads)
     out = torch.empty_like(q)
     flags = (_lib.ATTN_SEPARATE_COMBINE if separate else 0) | (_lib.ATTN_SPLIT_K if split_k else 0)
     status = lib.omni_verify_attention(
@@ -211,26 +223,30 @@ def verify_attention_static(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
 
 
 def draft_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor,
-                    tokens: int, keys: int, scale: float, **launch) -> torch.Tensor:
+                    tokens: int, keys: int, scale: float, *, tickets: torch.Tensor | None = None,
+                    **launch) -> torch.Tensor:
     """Draft verification: ``q`` [B*T, H, D], row b's T queries at rows b*T .. b*T+T-1; query i of row b attends to
     keys [0, lengths[b] + i) of cache row b (``k_cache``/``v_cache`` [>=B, H, S, D], all within the first ``keys``).
     One K/V read serves all T queries of a row.  Returns [B*T, H, D] in q's dtype.  ``launch``: overrides of
     ``DRAFT_ATTN`` (the reference's Triton settings -- block, warps, stages, programs -- have no meaning here and
-    are ignored).  (src/omniasr_trt/kernels.py:338-358)"""
+    are ignored).  ``tickets``: the caller's own merge tickets (B*H int32, zero; see :func:`_own_tickets`).
+    (src/omniasr_trt/kernels.py:338-358)"""
     cfg = {**DRAFT_ATTN, **{k: v for k, v in launch.items() if k in DRAFT_ATTN}}
-    return _verify(q, k_cache, v_cache, lengths, tokens, keys, scale, cfg["chunk"], cfg["separate"], cfg["split_k"])
+    return _verify(q, k_cache, v_cache, lengths, tokens, keys, scale, cfg["chunk"], cfg["separate"], cfg["split_k"],
+                   tickets)
 
 
 def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor,
                      keys: int, scale: float, block: int | None = None, warps: int | None = None,
-                     stages: int | None = None, programs: int | None = None, chunk: int | None = None) -> torch.Tensor:
+                     stages: int | None = None, programs: int | None = None, chunk: int | None = None, *,
+                     tickets: torch.Tensor | None = None) -> torch.Tensor:
     """``q`` [B, H, D]; ``k_cache``/``v_cache`` [>=B, H, S, D]; row r attends to keys [0, lengths[r]) (all within the
     first ``keys``, which fixes the launch grid).  Returns [B, H, D] in q's dtype.  ``block`` / ``warps`` /
     ``stages`` / ``programs`` are the reference's Triton settings, accepted and ignored.
     (src/omniasr_trt/kernels.py:406-423)"""
     del block, warps, stages, programs
     return _verify(q, k_cache, v_cache, lengths, 1, keys, scale, ATTN["chunk"] if chunk is None else chunk,
-                   ATTN["separate"], ATTN["split_k"])
+                   ATTN["separate"], ATTN["split_k"], tickets)
 
 
 class GenList:
@@ -268,12 +284,14 @@ def beam_gen_list(lst: GenList, ptr: torch.Tensor, gen_len: torch.Tensor, kg: to
 
 def beam_attention(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, ctx_len: torch.Tensor, kg: torch.Tensor,
                    vg: torch.Tensor, ptr: torch.Tensor, gen_len: torch.Tensor, beams: int, ctx_keys: int,
-                   scale: float, chunk: int = 0, gen_list: GenList | None = None) -> torch.Tensor:
+                   scale: float, chunk: int = 0, gen_list: GenList | None = None,
+                   tickets: torch.Tensor | None = None) -> torch.Tensor:
     """Beam rows ``q`` [S*N, H, D] (input g's beams are rows g*N .. g*N+N-1): attention over input g's context
     ``kc``/``vc`` [>=S, H, C, D] (first ``ctx_len[g]`` keys, all within ``ctx_keys``) and row r's generated keys
     ``kg``/``vg`` [>=S*N, H, G, D], position j read from row ``ptr[r, j]`` (first ``gen_len[r]``).  One pass over
     a group's context serves all of its beams.  Returns [S*N, H, D] in q's dtype.  ``gen_list``: the step's
     :func:`beam_gen_list` of the same pointers and lengths (optional; each shared generated key is then read once).
+    ``tickets``: the caller's own merge tickets (S*H int32, zero; see :func:`_own_tickets`).
     (src/omniasr_trt/kernels.py:309-332)"""
     lib = _lib.load()
     rows, heads, dim = q.shape
@@ -294,7 +312,7 @@ def beam_attention(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, ctx_len:
     _need(ctx_len.numel() >= groups and gen_len.numel() >= rows, "ctx_len: [S], gen_len: [S*N]")
     ws = lib.omni_beam_attention_workspace(groups, beams, heads, dim, ctx_keys, int(chunk))
     workspace = torch.empty(max(ws, 256), device=q.device, dtype=torch.uint8)
-    counters = _attn_counters(q.device, groups * heads)
+    counters = _own_tickets(tickets, q.device, groups * heads)
     out = torch.empty_like(q)
     args = (q.data_ptr(), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.size(2),
             ctx_len.data_ptr(), kg.data_ptr(), vg.data_ptr(), kg.stride(0), kg.stride(1), kg.stride(2), kg.size(2),

@@ -53,9 +53,10 @@ def test_beam_attention_inside_the_search(shape, monkeypatch):  # noqa: F811
     calls, checked = [0], []
     real = kernels.beam_attention
 
-    def recorded(q, kc, vc, ctx_len, kg, vg, ptr, gen_len, beams, ctx_keys, scale, chunk=0, gen_list=None):
-        assert gen_list is not None  # bf16: the step's list of distinct generated keys
-        out = real(q, kc, vc, ctx_len, kg, vg, ptr, gen_len, beams, ctx_keys, scale, chunk, gen_list)
+    def recorded(q, kc, vc, ctx_len, kg, vg, ptr, gen_len, beams, ctx_keys, scale, chunk=0, gen_list=None,
+                 tickets=None):
+        assert gen_list is not None and tickets is not None  # the step's list; the decoder's own tickets
+        out = real(q, kc, vc, ctx_len, kg, vg, ptr, gen_len, beams, ctx_keys, scale, chunk, gen_list, tickets)
         i = calls[0] % layers
         calls[0] += 1
         if i in (0, layers - 1) and len(checked) < 24:

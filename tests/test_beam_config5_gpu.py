@@ -71,9 +71,10 @@ def test_config5_beam_steps(cuda, monkeypatch):
         real_prepare(groups, beams, ctx, k_step, group_done, ptr, *out)
         rec["prepare_out"] = [host(t) for t in out] + [host(ptr)]
 
-    def attention(q, kc, vc, ctx_len, kg, vg, ptr, gen_len, beams, ctx_keys, scale, chunk=0, gen_list=None):
-        assert gen_list is not None  # bf16: the step's list of distinct generated keys
-        out = real_attn(q, kc, vc, ctx_len, kg, vg, ptr, gen_len, beams, ctx_keys, scale, chunk, gen_list)
+    def attention(q, kc, vc, ctx_len, kg, vg, ptr, gen_len, beams, ctx_keys, scale, chunk=0, gen_list=None,
+                  tickets=None):
+        assert gen_list is not None and tickets is dec.attn_tickets  # the step's list; the decoder's own tickets
+        out = real_attn(q, kc, vc, ctx_len, kg, vg, ptr, gen_len, beams, ctx_keys, scale, chunk, gen_list, tickets)
         i = rec["layer"]
         rec["layer"] += 1
         if i in (0, layers - 1):
@@ -129,5 +130,5 @@ def test_config5_beam_steps(cuda, monkeypatch):
             assert rec["layer"] == layers
             say(f"step {step}: generated keys {gen_len.max()}, scores {host(dec.score[:n]).round(3).tolist()}")
     assert rec["attn_checked"] == 2 * STEPS and rec["take_checked"] == STEPS
-    assert int(dec.select_tickets.abs().sum()) == 0
+    assert int(dec.select_tickets.abs().sum()) == 0 and int(dec.attn_tickets.abs().sum()) == 0
     dec.release()

@@ -115,6 +115,7 @@ def test_real_shape_drafted_steps(cuda, monkeypatch):
                 np.testing.assert_array_equal(after[name], o, err_msg=f"step {step}: {name}")
             say(f"step {step}: keys {keys}, advance {(after['last'] - before['last']).tolist()}")
     assert rec["checked"] == 2 * STEPS
+    assert int(dec.attn_tickets.abs().sum()) == 0  # the decoder's own merge tickets, left zero
     say(f"real shape: {STEPS} steps, attention and RoPE checked in layers {sorted(watch)}; {fragile_rows} argmax "
         f"rows lse-fragile")
     w.dec.release()
