@@ -20,12 +20,14 @@ from omniasr_trt_amd.modeling import HOP
 from omniasr_trt_amd.spec import SpecDecoder
 from omniasr_trt_amd.transcribe import Transcriber, frames_from_tokens
 
+from test_beam_gpu import ROBUST
 from test_decode_gpu import gpu_pair
 
 pytestmark = pytest.mark.gpu
 
 FRAMES = 100  # CTC frames per segment in these tests (the segment length is patched to 100 * HOP samples)
 VOCAB = 12
+SHAPES = [(17, 30, 9), (25,), (12, 40), (33, 8, 21, 14), (19,)]  # CTC frames of each input's segments
 
 
 def say(*a):
@@ -62,8 +64,7 @@ def oracle_transcripts(ref_dec, inputs, langs):
 def case(cuda):
     m, ref_dec = gpu_pair(24)
     g = torch.Generator().manual_seed(77)
-    shapes = [(17, 30, 9), (25,), (12, 40), (33, 8, 21, 14), (19,)]
-    inputs = [[torch.randn(f, 32, generator=g) for f in segs] for segs in shapes]
+    inputs = [[torch.randn(f, 32, generator=g) for f in segs] for segs in SHAPES]
     langs = [1, None, 3, 0, 4]
     ref = oracle_transcripts(ref_dec, inputs, [0 if x is None else x for x in langs])
     say(f"oracle tokens per segment: {[[len(t) for t in r] for r in ref]}")
@@ -139,3 +140,39 @@ def test_decoder_choice(case, monkeypatch):
         for i in range(len(audio)):
             row.tokens.append(direct.generate([t.context(row, i)])[0])
         assert got[j] == flat(row.tokens), j
+
+
+def oracle_beam_transcripts(ref_dec, inputs, langs, beams, length_norm):
+    """Per input the per-segment beam-search tokens, each segment's context built from the previous segment's."""
+    out = []
+    for audio, lang in zip(inputs, langs):
+        tokens = []
+        for i in range(len(audio)):
+            margins = []
+            ctx = oracle_context(ref_dec.sd, VOCAB, lang, audio, tokens, i)
+            tokens.append(oref.beam_reference(ref_dec, ctx, beams, length_norm, margins=margins))
+            assert min(margins) > ROBUST, f"segment {i} has a near-tie ({min(margins):.1e})"
+        out.append(tokens)
+    return out
+
+
+@pytest.mark.parametrize("beams,length_norm,seed", [(3, False, 77), (3, True, 89)])
+def test_beam_transcripts_vs_oracle(case, monkeypatch, beams, length_norm, seed):
+    """Beam transcription end to end (src tests/test_beam.py:45-62): every input's segments in order, segment i + 1's
+    context holding segment i's beam tokens, fewer groups than inputs (a finished group takes the next segment or
+    the next input), against the oracle's beam search of each segment's context in the reference's order.  The
+    inputs of each seed are chosen free of near-ties in the oracle's choices."""
+    m, _, langs, _ = case
+    monkeypatch.setattr(llm, "SEGMENT", FRAMES * HOP)
+    g = torch.Generator().manual_seed(seed)
+    inputs = [[torch.randn(f, 32, generator=g) for f in segs] for segs in SHAPES]
+    ref_dec = oref.Fp64Decoder(m)  # the case's own fp32 weights
+    want = [flat(r) for r in oracle_beam_transcripts(ref_dec, inputs, [0 if x is None else x for x in langs], beams,
+                                                     length_norm)]
+    say(f"transcriber: beams={beams} length_norm={length_norm}, {sum(map(len, want))} oracle tokens")
+    t = Transcriber(m, max_batch=2, reserve=16, beams=beams, length_norm=length_norm)
+    assert t.transcribe(inputs, langs) == want
+    assert isinstance(t.last_decoder, BeamDecoder) and t.last_decoder.beams == beams
+    # the same search asked for per call from a greedy transcriber
+    g = Transcriber(m, max_batch=2, reserve=16, draft_tokens=0)
+    assert g.transcribe(inputs, langs, beams=beams, length_norm=length_norm) == want
