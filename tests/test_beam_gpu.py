@@ -198,17 +198,21 @@ def test_beam_gen_list(cuda, beams, d):
         assert counts.sum() < total / 2  # the beams share most keys
 
 
-@pytest.mark.parametrize("h,d", [(32, 128), (8, 512)])
-def test_beam_attention_with_gen_list(cuda, h, d):
+@pytest.mark.parametrize("h,d,beams,gcap", [(32, 128, 5, 128), (8, 512, 5, 128), (32, 128, 11, 372),
+                                             (8, 512, 16, 256), (8, 512, 16, 257)])
+def test_beam_attention_with_gen_list(cuda, h, d, beams, gcap):
     """Both context kernels with the step's list of distinct generated keys: against the oracle and against the
     same call without the list, pointers shared like a beam search's, ragged generations, a finished input, an input
     with generated keys only; then captured in a graph with the list's build and replayed with new pointers and
-    lengths, every replay equal to the eager calls bit for bit; the tickets are left zero."""
-    groups, beams, gcap = 8, 5, 128
+    lengths, every replay equal to the eager calls bit for bit; the tickets are left zero.  The halves kernel's most
+    beams (11), a wide-head table of exactly 4096 keys (16 beams x 256), and one key more, where the generated keys
+    go to their own launch and the list is not read."""
+    groups = 8
     rows = groups * beams
+    say(f"gen list h={h} d={d} beams={beams} gen_cap={gcap}")
     ctx_len = torch.tensor([2000, 0, 333, 1500, 0, 900, 64, 1200])
-    gen_len = torch.randint(0, gcap + 1, (rows,), generator=torch.Generator().manual_seed(h))
-    gen_len[5:10] = 0  # input 1 finished
+    gen_len = torch.randint(0, gcap + 1, (rows,), generator=torch.Generator().manual_seed(h + beams))
+    gen_len[beams: 2 * beams] = 0  # input 1 finished
     q, kc, vc, kg, vg, _, cl, gl = _beam_inputs(torch.bfloat16, groups, beams, h, d, 2048, gcap, ctx_len, gen_len, 31)
     ptr = _shared_pointers(groups, beams, gcap, rows + 2, 32)
     want = ov.beam_attention(npf(q), npf(kc), npf(vc), cl.numpy(), npf(kg), npf(vg), ptr.numpy(), gl.numpy(), beams,
@@ -221,7 +225,7 @@ def test_beam_attention_with_gen_list(cuda, h, d):
     torch.cuda.synchronize()
     np.testing.assert_allclose(npf(got), want, atol=BF16_TOL[0], rtol=BF16_TOL[1])
     torch.testing.assert_close(got.float(), plain.float(), atol=1e-2, rtol=1e-2)
-    assert torch.all(got[5:10] == 0)
+    assert torch.all(got[beams: 2 * beams] == 0)
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     graph = torch.cuda.CUDAGraph()
