@@ -169,14 +169,16 @@ def test_verify_attention_wide_heads_up_to_32_queries(cuda, t, d):
 @pytest.mark.parametrize("width,d,b,h", [(1, 128, 3, 4), (15, 128, 3, 4), (64, 128, 3, 4), (97, 128, 3, 4),
                                          (300, 128, 3, 4), (1, 512, 3, 4), (15, 512, 3, 4), (96, 512, 3, 4),
                                          (97, 512, 3, 4), (300, 512, 3, 4), (1, 256, 3, 4), (192, 256, 3, 4),
-                                         (300, 256, 3, 4), (300, 128, 4, 2), (400, 512, 2, 4), (250, 256, 8, 1)])
+                                         (300, 256, 3, 4), (300, 128, 4, 2), (400, 512, 2, 4), (250, 256, 8, 1),
+                                         (256, 128, 2, 2), (513, 128, 2, 3), (1100, 128, 1, 8)])
 def test_prefill_attention(cuda, width, d, b, h):
     """Causal attention over whole contexts (src/omniasr_trt/decode.py:163-164) against the oracle's verify attention
     with query p of a context over keys [0, p]: cache rows addressed through slots, widths that are not multiples
     of the query block (192 queries at head dims 128 and 256, 96 at 512) or of the 32-key tile; heads x contexts a
-    multiple of 8 (the XCD-ordered workgroup map) or not (the plain one)."""
+    multiple of 8 (the XCD-ordered workgroup map) or not (the plain one); at head dim 128 also widths past one
+    block and up to six blocks."""
     g = gen(60 + width)
-    rows, cap = 5, 448
+    rows, cap = 5, max(448, -(-width // 64) * 64)
     kc = torch.randn(rows, h, cap, d, generator=g).to(torch.bfloat16)
     vc = torch.randn(rows, h, cap, d, generator=g).to(torch.bfloat16)
     q = torch.randn(b * width, h, d, generator=g).to(torch.bfloat16)
