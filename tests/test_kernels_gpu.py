@@ -118,6 +118,25 @@ def test_verify_attention_bf16(cuda, t):
     _attn_case(cuda, torch.bfloat16, 4, 4, 256, t, 700, lengths, 640, 5, BF16_TOL)  # two 128-dimension slices
 
 
+@pytest.mark.parametrize("b,keys", [(1, 256), (3, 1024), (8, 2048), (16, 512)])
+def test_decode_attention_reference_cases(cuda, b, keys):
+    """The reference's own decode-attention cases (src tests/test_kernels.py:42-55): fp32, 8 heads x 512, a cache of
+    2048 positions, lengths U[1, keys] with row 0 at ``keys`` (the whole bucket; at 2048 the whole cache), within the
+    reference's tolerance of 2e-5 of the fp64 oracle."""
+    g = gen(b * 7 + keys)
+    h, d, cap = 8, 512, 2048
+    kc = torch.randn(b + 1, h, cap, d, generator=g)
+    vc = torch.randn(b + 1, h, cap, d, generator=g)
+    q = torch.randn(b, h, d, generator=g)
+    lengths = torch.randint(1, keys + 1, (b,), generator=g)
+    lengths[0] = keys
+    say(f"decode_attention reference case b={b} keys={keys}")
+    out = kernels.decode_attention(q.to(cuda), kc.to(cuda), vc.to(cuda), lengths.to(cuda), keys, d ** -0.5)
+    torch.cuda.synchronize()
+    want = ov.verify_attention(npf(q), npf(kc)[:b], npf(vc)[:b], lengths.numpy(), 1, d ** -0.5)
+    np.testing.assert_allclose(npf(out), want, atol=2e-5, rtol=2e-5)
+
+
 @pytest.mark.parametrize("dtype,rows,heads,d", [(torch.bfloat16, 8, 32, 128), (torch.bfloat16, 3, 4, 128),
                                                  (torch.bfloat16, 8, 8, 512), (torch.float32, 5, 4, 64),
                                                  (torch.float32, 4, 2, 512)])
