@@ -74,6 +74,16 @@ def test_beam_attention_f32(cuda, beams, d):
     _beam_case(cuda, torch.float32, 3, beams, 2, d, 300, 70, [300, 65, 0], gen_len, 320, 10, F32_TOL)
 
 
+@pytest.mark.parametrize("beams", [1, 3, 5])
+def test_beam_attention_f32_reference_case(cuda, beams):
+    """The reference's fp32 case (tests/test_kernels.py:98-126) at its shape: 4 inputs x 8 heads x 512, contexts
+    [600, 333, 1, 0] in a cache of 600, 300 generated positions, the last input finished, within its 1e-4."""
+    gen_len = torch.randint(0, 300, (4 * beams,), generator=torch.Generator().manual_seed(20 + beams))
+    gen_len[-beams:] = 0
+    out = _beam_case(cuda, torch.float32, 4, beams, 8, 512, 600, 300, [600, 333, 1, 0], gen_len, 640, 21, F32_TOL)
+    assert torch.all(out[-beams:] == 0)
+
+
 def test_beam_attention_config5(cuda):
     """Config 5 (beam variant): 8 inputs x 5 beams, 32 heads x 128, contexts U[750, 2400], 1-160 generated keys;
     several split sizes."""
